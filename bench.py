@@ -1,0 +1,235 @@
+"""Benchmark of the fused attention forward on one MI355X.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
+                  [--no-cpu-baseline] [--all]
+
+A step is one fused forward over one batch of synthetic input (the hot path:
+flash_attention_sm75.flash_attention_forward -> flash_attn_sm75_cuda ->
+fa_sm75_forward -> one kernel launch).  Inputs are generated from a seeded CPU
+generator, copied to HBM before the timed region, and stay resident.
+
+Metric: forward TFLOPS with FLOP = 4*B*Hq*N^2*D, halved for
+causal (reference benchmarks/benchmark_attention.py:78-82), and its fraction
+of the dense fp16 MFMA peak (2.5 PFLOP/s).  The default workload is C4, the
+configuration the north-star target is quoted on (B=1 Hq=32 Hkv=8 N=8192
+D=128 causal).
+
+Printed: ONE JSON line on stdout (rank 0).  Besides the driver's keys it holds
+  roofline      the kernel's average launch time (HIP events around each
+                launch, on the launch stream) against the MFMA peak; traffic
+                is the HBM bytes per launch from the committed rocprofv3
+                FETCH_SIZE/WRITE_SIZE summary for this workload, when present;
+  cpu_baseline  the reference math path (restated with torch on the host
+                CPU) timed on a bounded sample of the same workload.
+Diagnostics go to stderr.
+"""
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG_SRC = os.path.join(REPO, "flash-attention-sm75-register-fused_amd", "src")
+for _p in (PKG_SRC, REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+# name -> (B, Hq, Hkv, N, D, causal, std, k_stress)
+CONFIGS = {
+    "C1": (1, 1, 1, 512, 64, False, 1.0, False),
+    "C2": (4, 12, 12, 1024, 64, False, 1.0, False),
+    "C3": (4, 8, 8, 2048, 64, True, 1.0, False),
+    "C4": (1, 32, 8, 8192, 128, True, 1.0, False),
+    "C5": (2, 64, 8, 16384, 128, True, 0.5, True),
+}
+DESCR = {
+    "C1": "full attention fwd B=1 H=1 N=512 d=64",
+    "C2": "full attention fwd B=4 H=12 N=1024 d=64",
+    "C3": "causal attention fwd B=4 H=8 N=2048 d=64",
+    "C4": "causal GQA prefill fwd B=1 Hq=32 Hkv=8 N=8192 d=128",
+    "C5": "long-context causal GQA fwd B=2 Hq=64 Hkv=8 N=16384 d=128, K x4 on 5% rows",
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def flops(B, Hq, N, D, causal):
+    f = 4 * B * Hq * N * N * D
+    return f // 2 if causal else f
+
+
+def min_bytes(B, Hq, Hkv, N, D):
+    return 2 * (B * Hq * N * D) * 2 + 2 * (B * Hkv * N * D) * 2
+
+
+def make_inputs(cfg, seed=0):
+    import torch
+
+    B, Hq, Hkv, N, D, causal, std, stress = CONFIGS[cfg]
+    g = torch.Generator("cpu").manual_seed(seed)
+    q = (torch.randn(B, Hq, N, D, generator=g) * std).half()
+    k = torch.randn(B, Hkv, N, D, generator=g) * std
+    v = (torch.randn(B, Hkv, N, D, generator=g) * std).half()
+    if stress:
+        rows = torch.rand(B, Hkv, N, generator=g) < 0.05
+        k = torch.where(rows[..., None], k * 4, k)
+    return q, k.half(), v
+
+
+def read_traffic(cfg):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary."""
+    path = os.path.join(REPO, "profiles", f"fa_fwd_{cfg.lower()}_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def time_gpu(cfg, steps, warmup):
+    import torch
+
+    from flash_attention_sm75 import flash_attention_forward
+
+    B, Hq, Hkv, N, D, causal, _, _ = CONFIGS[cfg]
+    dev = torch.device("cuda", 0)
+    q, k, v = (t.to(dev) for t in make_inputs(cfg))
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        flash_attention_forward(q, k, v, causal=causal)
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        flash_attention_forward(q, k, v, causal=causal)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    return wall, kern_ms
+
+
+def cpu_baseline(cfg, budget_s=20.0):
+    """Reference math path (torch on the host CPU) on a bounded sample:
+    whole query heads of the workload, as many as fit in ``budget_s``."""
+    import torch
+
+    from oracle import attention_ref as ref
+
+    B, Hq, Hkv, N, D, causal, _, _ = CONFIGS[cfg]
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    q, k, v = make_inputs(cfg)
+    done, t_used, b = 0, 0.0, 0
+    heads = []
+    while t_used < budget_s and done < B * Hq:
+        b, h = divmod(done, Hq)
+        t0 = time.perf_counter()
+        ref.attention_reference_torch_cpu(q[b:b + 1], k[b:b + 1], v[b:b + 1], causal=causal,
+                                          heads=[h])
+        t_used += time.perf_counter() - t0
+        heads.append((b, h))
+        done += 1
+    f = flops(1, done, N, D, causal)
+    return {
+        "value": f / t_used / 1e12,
+        "unit": "TFLOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{done} of {B * Hq} (batch, query-head) slices of {cfg}, all {N} rows each, "
+                   f"{t_used:.1f} s; torch CPU restatement of reference "
+                   f"src/reference/attention_ref.py (fp32, full NxN scores then causal mask)"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C4", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--all", action="store_true", help="also time C1..C5 (stderr)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    cfg = args.config
+    B, Hq, Hkv, N, D, causal, _, _ = CONFIGS[cfg]
+    F = flops(B, Hq, N, D, causal)
+
+    if args.all:
+        for c in sorted(CONFIGS):
+            b_, hq_, hkv_, n_, d_, ca_, _, _ = CONFIGS[c]
+            w, km = time_gpu(c, 10, 3)
+            med = km[len(km) // 2]
+            log(f"[{c}] {DESCR[c]}: median kernel {med:.4f} ms -> "
+                f"{flops(b_, hq_, n_, d_, ca_) / med / 1e9:.1f} TFLOPS")
+
+    wall, kern_ms = time_gpu(cfg, args.steps, args.warmup)
+    ms_per_step = wall * 1e3 / args.steps
+    avg_kernel_ms = sum(kern_ms) / len(kern_ms)
+    value = F * args.steps / wall / 1e12
+    achieved = F / (avg_kernel_ms * 1e-3) / 1e12
+    log(f"[{cfg}] wall {ms_per_step:.4f} ms/step, kernel avg {avg_kernel_ms:.4f} ms "
+        f"(median {kern_ms[len(kern_ms) // 2]:.4f}, min {kern_ms[0]:.4f}) -> "
+        f"{value:.1f} TFLOPS wall, {achieved:.1f} TFLOPS kernel")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg, args.cpu_budget)
+        log(f"[cpu] {cpu}")
+
+    traffic = read_traffic(cfg)
+    line = {
+        "metric": "fwd attention TFLOPS & % fp16 MFMA peak (1 GPU), full + causal, d64/d128",
+        "value": round(value, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded CPU generator, N(0,1) fp16, resident in HBM)",
+        "config": {
+            "workload": f"{cfg}: {DESCR[cfg]}",
+            "batch": B, "heads_q": Hq, "heads_kv": Hkv, "seq_len": N, "head_dim": D,
+            "causal": causal, "flop_per_step": F, "parallelism": "none (1 GPU)",
+        },
+        "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": min_bytes(B, Hq, Hkv, N, D),
+            "kernel_avg_ms": round(avg_kernel_ms, 5),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,166 @@
+// PyTorch binding: module `flash_attn_sm75_cuda`.
+//
+// Same op names, signatures and error texts as the reference binding
+// (reference src/bindings/pytorch_extension.cpp:21-129):
+//   naive_attention_forward, flash_attention_forward,
+//   flash_attention_forward_scalar, flash_attention_forward_wmma_qk,
+// each (Tensor Q, Tensor K, Tensor V, bool causal, float scale) -> Tensor.
+// Additions: flash_attention_forward accepts grouped K/V heads (Hkv divides
+// Hq) so no repeat_interleave copy is needed, and flash_attention_forward_lse
+// also returns the fp32 row log-sum-exp.
+//
+// All checks run before any device work; the kernels are enqueued on the
+// current HIP stream of Q's device and the host is not blocked.
+#include <torch/extension.h>
+
+#include <ATen/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <string>
+#include <tuple>
+
+#include "flash_attn_sm75.h"
+
+namespace {
+
+void check_tensor(const torch::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), std::string(name) + " must be a CUDA tensor");
+  TORCH_CHECK(t.dtype() == torch::kFloat16, std::string(name) + " must be FP16");
+  TORCH_CHECK(t.is_contiguous(), std::string(name) + " must be contiguous");
+  TORCH_CHECK(t.dim() == 4, std::string(name) + " must be [B, H, N, D]");
+}
+
+void check_same_device(const torch::Tensor& Q, const torch::Tensor& K,
+                       const torch::Tensor& V) {
+  TORCH_CHECK(Q.device() == K.device() && Q.device() == V.device(),
+              "Q, K, V must be on the same device");
+}
+
+fa_fwd_params make_params(const torch::Tensor& Q, const torch::Tensor& K,
+                          const torch::Tensor& V, torch::Tensor& O, float* lse,
+                          bool causal, float scale) {
+  fa_fwd_params p{};
+  p.q = reinterpret_cast<const fa_half*>(Q.data_ptr<at::Half>());
+  p.k = reinterpret_cast<const fa_half*>(K.data_ptr<at::Half>());
+  p.v = reinterpret_cast<const fa_half*>(V.data_ptr<at::Half>());
+  p.o = reinterpret_cast<fa_half*>(O.data_ptr<at::Half>());
+  p.lse = lse;
+  p.batch = Q.size(0);
+  p.heads_q = Q.size(1);
+  p.heads_kv = K.size(1);
+  p.seq_len = Q.size(2);
+  p.head_dim = Q.size(3);
+  p.q_stride_b = Q.stride(0); p.q_stride_h = Q.stride(1); p.q_stride_n = Q.stride(2);
+  p.k_stride_b = K.stride(0); p.k_stride_h = K.stride(1); p.k_stride_n = K.stride(2);
+  p.v_stride_b = V.stride(0); p.v_stride_h = V.stride(1); p.v_stride_n = V.stride(2);
+  p.o_stride_b = O.stride(0); p.o_stride_h = O.stride(1); p.o_stride_n = O.stride(2);
+  p.scale = scale;
+  p.causal = causal ? 1 : 0;
+  p.stream = nullptr;
+  return p;
+}
+
+// Shape checks of the fused op (reference pytorch_extension.cpp:56-68), with
+// the heads check widened from equality to divisibility.
+void check_fused_shapes(const torch::Tensor& Q, const torch::Tensor& K,
+                        const torch::Tensor& V) {
+  check_tensor(Q, "Q");
+  check_tensor(K, "K");
+  check_tensor(V, "V");
+  check_same_device(Q, K, V);
+  TORCH_CHECK(Q.size(0) == K.size(0), "batch mismatch");
+  TORCH_CHECK(K.size(1) > 0 && Q.size(1) % K.size(1) == 0,
+              "heads mismatch after GQA expansion: Q heads (", Q.size(1),
+              ") not divisible by K/V heads (", K.size(1), ")");
+  TORCH_CHECK(Q.size(2) == K.size(2), "seq_len mismatch");
+  TORCH_CHECK(Q.size(3) == K.size(3), "head_dim mismatch");
+  TORCH_CHECK(K.sizes() == V.sizes(), "K and V must have identical shapes");
+  const auto head_dim = Q.size(3);
+  TORCH_CHECK(head_dim == 64 || head_dim == 128,
+              "flash_attention_forward supports head_dim=64 or 128, got ", head_dim);
+}
+
+void run_fused(const torch::Tensor& Q, const torch::Tensor& K, const torch::Tensor& V,
+               torch::Tensor& O, float* lse, bool causal, float scale) {
+  const at::OptionalDeviceGuard guard(at::device_of(Q));
+  fa_fwd_params p = make_params(Q, K, V, O, lse, causal, scale);
+  p.stream = c10::hip::getCurrentHIPStream(Q.device().index()).stream();
+  const int st = fa_sm75_forward(&p);
+  TORCH_CHECK(st == FA_OK, "flash_attention_forward: ", fa_sm75_last_error());
+}
+
+torch::Tensor flash_attention_forward(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                      bool causal, float scale) {
+  check_fused_shapes(Q, K, V);
+  auto O = torch::empty_like(Q);
+  run_fused(Q, K, V, O, nullptr, causal, scale);
+  return O;
+}
+
+std::tuple<torch::Tensor, torch::Tensor> flash_attention_forward_lse(
+    torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal, float scale) {
+  check_fused_shapes(Q, K, V);
+  auto O = torch::empty_like(Q);
+  auto L = torch::empty({Q.size(0), Q.size(1), Q.size(2)},
+                        Q.options().dtype(torch::kFloat32));
+  run_fused(Q, K, V, O, L.data_ptr<float>(), causal, scale);
+  return {O, L};
+}
+
+torch::Tensor d64_compat(const char* tag, torch::Tensor Q, torch::Tensor K,
+                         torch::Tensor V, bool causal, float scale) {
+  check_tensor(Q, "Q");
+  check_tensor(K, "K");
+  check_tensor(V, "V");
+  check_same_device(Q, K, V);
+  TORCH_CHECK(Q.sizes() == K.sizes() && Q.sizes() == V.sizes(),
+              "Q, K, V must have identical shapes");
+  TORCH_CHECK(Q.size(3) == 64, tag, " kernel supports head_dim=64 only");
+  auto O = torch::empty_like(Q);
+  run_fused(Q, K, V, O, nullptr, causal, scale);
+  return O;
+}
+
+// reference pytorch_extension.cpp:84-102
+torch::Tensor flash_attention_forward_scalar(torch::Tensor Q, torch::Tensor K,
+                                             torch::Tensor V, bool causal, float scale) {
+  return d64_compat("scalar", Q, K, V, causal, scale);
+}
+
+// reference pytorch_extension.cpp:104-122
+torch::Tensor flash_attention_forward_wmma_qk(torch::Tensor Q, torch::Tensor K,
+                                              torch::Tensor V, bool causal, float scale) {
+  return d64_compat("wmma_qk", Q, K, V, causal, scale);
+}
+
+// reference pytorch_extension.cpp:28-50
+torch::Tensor naive_attention_forward(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                      bool causal, float scale) {
+  check_tensor(Q, "Q");
+  check_tensor(K, "K");
+  check_tensor(V, "V");
+  check_same_device(Q, K, V);
+  TORCH_CHECK(Q.sizes() == K.sizes() && Q.sizes() == V.sizes(),
+              "naive_attention: Q, K, V must have identical shapes");
+  auto O = torch::empty_like(Q);
+  auto ws = torch::empty({Q.size(0) * Q.size(1), Q.size(2), Q.size(2)},
+                         Q.options().dtype(torch::kFloat32));
+  const at::OptionalDeviceGuard guard(at::device_of(Q));
+  fa_fwd_params p = make_params(Q, K, V, O, nullptr, causal, scale);
+  p.stream = c10::hip::getCurrentHIPStream(Q.device().index()).stream();
+  const int st = fa_sm75_naive_forward(&p, ws.data_ptr<float>());
+  TORCH_CHECK(st == FA_OK, "naive_attention_forward: ", fa_sm75_last_error());
+  return O;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "MI355X (gfx950) fused attention forward, reference-compatible op set";
+  m.def("naive_attention_forward", &naive_attention_forward);
+  m.def("flash_attention_forward", &flash_attention_forward);
+  m.def("flash_attention_forward_scalar", &flash_attention_forward_scalar);
+  m.def("flash_attention_forward_wmma_qk", &flash_attention_forward_wmma_qk);
+  m.def("flash_attention_forward_lse", &flash_attention_forward_lse);
+  m.def("abi_version", []() { return fa_sm75_abi_version(); });
+}

@@ -1,0 +1,238 @@
+// C ABI of the library: argument validation, status codes, the stream-ordered
+// entry points and the four reference-signature launchers.
+//
+// Every check runs before the first HIP call, so all error paths are
+// reachable without a device.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "fa_internal.h"
+#include "flash_attn_sm75.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Shared validation of the fused and naive entry points.
+int validate(const fa_fwd_params* p, bool fused) {
+  if (p == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "params must not be NULL");
+  if (p->batch < 0 || p->heads_q < 0 || p->heads_kv < 0 || p->seq_len < 0 ||
+      p->head_dim < 0)
+    return fail(FA_ERR_INVALID_ARGUMENT,
+                "sizes must be non-negative (batch=%lld heads_q=%lld heads_kv=%lld "
+                "seq_len=%lld head_dim=%lld)",
+                (long long)p->batch, (long long)p->heads_q, (long long)p->heads_kv,
+                (long long)p->seq_len, (long long)p->head_dim);
+  if (fused) {
+    if (p->head_dim != 64 && p->head_dim != 128)
+      return fail(FA_ERR_UNSUPPORTED_HEAD_DIM,
+                  "flash_attention_forward supports head_dim=64 or 128, got %lld",
+                  (long long)p->head_dim);
+  } else {
+    if (p->head_dim < 1 || p->head_dim > 256 || (p->head_dim % 8) != 0)
+      return fail(FA_ERR_UNSUPPORTED_HEAD_DIM,
+                  "naive_attention supports head_dim multiple of 8 in [8, 256], got %lld",
+                  (long long)p->head_dim);
+  }
+  if (p->heads_q > 0 && p->heads_kv == 0)
+    return fail(FA_ERR_HEADS_NOT_DIVISIBLE, "heads_kv must be positive");
+  if (p->heads_kv > 0 && (p->heads_q % p->heads_kv) != 0)
+    return fail(FA_ERR_HEADS_NOT_DIVISIBLE,
+                "heads mismatch: Q heads (%lld) not divisible by K/V heads (%lld)",
+                (long long)p->heads_q, (long long)p->heads_kv);
+  if (!std::isfinite(p->scale))
+    return fail(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  const bool empty = p->batch == 0 || p->heads_q == 0 || p->seq_len == 0;
+  if (empty) return FA_OK;
+  if (!p->q || !p->k || !p->v || !p->o)
+    return fail(FA_ERR_INVALID_ARGUMENT, "Q, K, V and O pointers must not be NULL");
+  if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o))
+    return fail(FA_ERR_MISALIGNED, "Q, K, V and O must be 16-byte aligned");
+  const int64_t strides[12] = {p->q_stride_b, p->q_stride_h, p->q_stride_n,
+                               p->k_stride_b, p->k_stride_h, p->k_stride_n,
+                               p->v_stride_b, p->v_stride_h, p->v_stride_n,
+                               p->o_stride_b, p->o_stride_h, p->o_stride_n};
+  for (int i = 0; i < 12; ++i) {
+    if (strides[i] < 0)
+      return fail(FA_ERR_INVALID_ARGUMENT, "strides must be non-negative");
+    if (strides[i] % 8 != 0)
+      return fail(FA_ERR_MISALIGNED,
+                  "batch/head/row strides must be multiples of 8 elements (16 bytes)");
+  }
+  if (p->q_stride_n < p->head_dim || p->k_stride_n < p->head_dim ||
+      p->v_stride_n < p->head_dim || p->o_stride_n < p->head_dim)
+    return fail(FA_ERR_INVALID_ARGUMENT, "row stride must be at least head_dim");
+  if (p->seq_len > (int64_t)fa::fused_block_m() * 65535 || p->seq_len > INT32_MAX / 2)
+    return fail(FA_ERR_TOO_LARGE, "seq_len %lld exceeds the supported maximum",
+                (long long)p->seq_len);
+  if (p->batch * p->heads_q > (int64_t)(1u << 24))
+    return fail(FA_ERR_TOO_LARGE, "batch*heads_q %lld exceeds 2^24",
+                (long long)(p->batch * p->heads_q));
+  return FA_OK;
+}
+
+fa::FwdArgs make_args(const fa_fwd_params* p) {
+  fa::FwdArgs a;
+  a.q = reinterpret_cast<const _Float16*>(p->q);
+  a.k = reinterpret_cast<const _Float16*>(p->k);
+  a.v = reinterpret_cast<const _Float16*>(p->v);
+  a.o = reinterpret_cast<_Float16*>(p->o);
+  a.lse = p->lse;
+  a.qsb = p->q_stride_b; a.qsh = p->q_stride_h; a.qsn = p->q_stride_n;
+  a.ksb = p->k_stride_b; a.ksh = p->k_stride_h; a.ksn = p->k_stride_n;
+  a.vsb = p->v_stride_b; a.vsh = p->v_stride_h; a.vsn = p->v_stride_n;
+  a.osb = p->o_stride_b; a.osh = p->o_stride_h; a.osn = p->o_stride_n;
+  a.n = (int)p->seq_len;
+  a.hq = (int)p->heads_q;
+  a.group = (int)(p->heads_kv > 0 ? p->heads_q / p->heads_kv : 1);
+  a.num_qblocks = 0;
+  const float log2e = 1.4426950408889634f;
+  float c = std::fabs(p->scale) * log2e;
+  // scale == 0 must still give uniform weights over the visible keys; a tiny
+  // positive factor keeps exp2(-inf * c) = 0 for masked keys.
+  if (c < 1e-30f) c = 1e-30f;
+  a.c = c;
+  a.negate_q = p->scale < 0.0f ? 1 : 0;
+  return a;
+}
+
+int check_launch() {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(FA_ERR_HIP, "HIP launch failed: %s", hipGetErrorString(e));
+  return FA_OK;
+}
+
+// Shared body of the reference-signature launchers: contiguous, default
+// stream, synchronous, message on stderr on failure.
+void legacy_launch(const char* tag, const fa_half* Q, const fa_half* K, const fa_half* V,
+                   fa_half* O, int batch, int heads, int seq_len, int head_dim,
+                   float scale, bool causal, bool d64_only, float* workspace) {
+  if (d64_only && head_dim != 64) {
+    std::fprintf(stderr, "[%s] head_dim=%d not supported\n", tag, head_dim);
+    return;
+  }
+  fa_fwd_params p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = Q; p.k = K; p.v = V; p.o = O;
+  p.batch = batch; p.heads_q = heads; p.heads_kv = heads;
+  p.seq_len = seq_len; p.head_dim = head_dim;
+  fa_sm75_set_contiguous_strides(&p);
+  p.scale = scale;
+  p.causal = causal ? 1 : 0;
+  p.stream = nullptr;
+  const int st = workspace ? fa_sm75_naive_forward(&p, workspace) : fa_sm75_forward(&p);
+  if (st != FA_OK) {
+    std::fprintf(stderr, "[%s] %s\n", tag, fa_sm75_last_error());
+    return;
+  }
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) std::fprintf(stderr, "[%s] %s\n", tag, hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+void fa_sm75_set_contiguous_strides(fa_fwd_params* p) {
+  const int64_t D = p->head_dim, N = p->seq_len;
+  p->q_stride_n = D; p->q_stride_h = N * D; p->q_stride_b = p->heads_q * N * D;
+  p->o_stride_n = D; p->o_stride_h = N * D; p->o_stride_b = p->heads_q * N * D;
+  p->k_stride_n = D; p->k_stride_h = N * D; p->k_stride_b = p->heads_kv * N * D;
+  p->v_stride_n = D; p->v_stride_h = N * D; p->v_stride_b = p->heads_kv * N * D;
+}
+
+int fa_sm75_forward(const fa_fwd_params* p) {
+  g_last_error[0] = '\0';
+  const int st = validate(p, true);
+  if (st != FA_OK) return st;
+  if (p->batch == 0 || p->heads_q == 0 || p->seq_len == 0) return FA_OK;
+  const fa::FwdArgs a = make_args(p);
+  fa::launch_fused_forward(a, (int)p->batch, (int)p->head_dim, p->causal != 0,
+                           reinterpret_cast<hipStream_t>(p->stream));
+  return check_launch();
+}
+
+int fa_sm75_naive_forward(const fa_fwd_params* p, float* workspace) {
+  g_last_error[0] = '\0';
+  const int st = validate(p, false);
+  if (st != FA_OK) return st;
+  if (p->batch == 0 || p->heads_q == 0 || p->seq_len == 0) return FA_OK;
+  if (workspace == nullptr)
+    return fail(FA_ERR_INVALID_ARGUMENT, "workspace must not be NULL");
+  if (p->lse != nullptr)
+    return fail(FA_ERR_INVALID_ARGUMENT, "the naive path does not produce LSE");
+  if (p->seq_len > 65535)
+    return fail(FA_ERR_TOO_LARGE, "naive path supports seq_len <= 65535");
+  const fa::FwdArgs a = make_args(p);
+  fa::launch_naive_forward(a, (int)p->batch, (int)p->head_dim, p->causal != 0, p->scale,
+                           workspace, reinterpret_cast<hipStream_t>(p->stream));
+  return check_launch();
+}
+
+const char* fa_sm75_last_error(void) { return g_last_error; }
+
+const char* fa_sm75_status_string(int status) {
+  switch (status) {
+    case FA_OK: return "ok";
+    case FA_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case FA_ERR_UNSUPPORTED_HEAD_DIM: return "unsupported head_dim";
+    case FA_ERR_HEADS_NOT_DIVISIBLE: return "heads_q not divisible by heads_kv";
+    case FA_ERR_MISALIGNED: return "misaligned pointer or stride";
+    case FA_ERR_TOO_LARGE: return "problem too large";
+    case FA_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+int fa_sm75_abi_version(void) { return FA_SM75_ABI_VERSION; }
+
+void launch_flash_attention_forward(const fa_half* Q, const fa_half* K, const fa_half* V,
+                                    fa_half* O, int batch, int heads, int seq_len,
+                                    int head_dim, float scale, bool causal) {
+  legacy_launch("flash_attn", Q, K, V, O, batch, heads, seq_len, head_dim, scale, causal,
+                false, nullptr);
+}
+
+void launch_flash_attention_forward_scalar(const fa_half* Q, const fa_half* K,
+                                           const fa_half* V, fa_half* O, int batch,
+                                           int heads, int seq_len, int head_dim,
+                                           float scale, bool causal) {
+  legacy_launch("flash_attn_scalar", Q, K, V, O, batch, heads, seq_len, head_dim, scale,
+                causal, true, nullptr);
+}
+
+void launch_flash_attention_forward_wmma_qk(const fa_half* Q, const fa_half* K,
+                                            const fa_half* V, fa_half* O, int batch,
+                                            int heads, int seq_len, int head_dim,
+                                            float scale, bool causal) {
+  legacy_launch("flash_attn_wmma_qk", Q, K, V, O, batch, heads, seq_len, head_dim, scale,
+                causal, true, nullptr);
+}
+
+void launch_naive_attention(const fa_half* Q, const fa_half* K, const fa_half* V,
+                            fa_half* O, int batch, int heads, int seq_len, int head_dim,
+                            float scale, bool causal, float* workspace) {
+  if (workspace == nullptr) {
+    std::fprintf(stderr, "[naive_attention] workspace must not be NULL\n");
+    return;
+  }
+  legacy_launch("naive_attention", Q, K, V, O, batch, heads, seq_len, head_dim, scale,
+                causal, false, workspace);
+}
+
+}  // extern "C"

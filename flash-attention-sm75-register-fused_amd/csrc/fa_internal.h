@@ -1,0 +1,37 @@
+// Internal interface between the C ABI (fa_capi.hip) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+// Kernel arguments of the fused forward (passed by value).
+struct FwdArgs {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* v;
+  _Float16* o;
+  float* lse;  // [B*Hq, N] or nullptr
+  int64_t qsb, qsh, qsn;
+  int64_t ksb, ksh, ksn;
+  int64_t vsb, vsh, vsn;
+  int64_t osb, osh, osn;
+  int n;            // sequence length (queries == keys)
+  int hq;           // query heads
+  int group;        // heads_q / heads_kv
+  int num_qblocks;  // filled by the launcher
+  float c;          // |scale| * log2(e), clamped away from 0
+  int negate_q;     // scale < 0: Q fragments are negated (exact in fp16)
+};
+
+// Launches the fused MFMA kernel; all arguments already validated.
+int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
+                         hipStream_t stream);
+int fused_block_m();
+
+// Three-kernel path through an fp32 [B*Hq, N, N] score workspace.
+int launch_naive_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
+                         float scale, float* workspace, hipStream_t stream);
+
+}  // namespace fa

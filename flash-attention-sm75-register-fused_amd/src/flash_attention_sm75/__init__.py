@@ -1,0 +1,8 @@
+"""MI355X-native drop-in for the `flash_attention_sm75` package.
+
+Public surface identical to reference src/flash_attention_sm75/__init__.py:1-4.
+"""
+from .ops import flash_attention_forward, flash_attention_forward_lse
+
+__version__ = "0.1.0"
+__all__ = ["flash_attention_forward", "flash_attention_forward_lse"]

@@ -1,0 +1,108 @@
+"""Python API of the fused attention forward (gfx950).
+
+Mirrors reference src/flash_attention_sm75/ops.py:1-82: same names, defaults,
+argument meaning and error texts.  One behavioural difference, by design:
+grouped-query attention no longer materialises ``repeat_interleave`` copies of
+K and V (reference ops.py:24-26); the kernel maps query head ``h`` to KV head
+``h // (Hq // Hkv)`` by index, which is the same mapping.
+
+The native module ``flash_attn_sm75_cuda`` is required: importing this
+package without it raises ImportError (there is no CPU fallback).
+"""
+import math
+
+import torch
+
+import flash_attn_sm75_cuda as _C
+
+
+def _expand_kv_for_gqa(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor):
+    """Explicit GQA/MQA expansion of K and V to Q's head count.
+
+    Kept for callers of the reference helper (reference ops.py:6-27).  The
+    forward path does not call it; it only checks divisibility with
+    :func:`_check_gqa_heads`.
+    """
+    _check_gqa_heads(Q, K)
+    h_q, h_kv = Q.size(1), K.size(1)
+    if h_q == h_kv:
+        return K, V
+    factor = h_q // h_kv
+    K = K.repeat_interleave(factor, dim=1).contiguous()
+    V = V.repeat_interleave(factor, dim=1).contiguous()
+    return K, V
+
+
+def _check_gqa_heads(Q: torch.Tensor, K: torch.Tensor) -> None:
+    h_q, h_kv = Q.size(1), K.size(1)
+    if h_kv == 0 or h_q % h_kv != 0:
+        raise RuntimeError(
+            f"GQA expansion: Q heads ({h_q}) not divisible by K/V heads ({h_kv})"
+        )
+
+
+class FlashAttentionSM75Function(torch.autograd.Function):
+    """Forward-only autograd function (reference ops.py:30-52)."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, causal, scale):
+        _check_gqa_heads(Q, K)
+        Q = Q.contiguous()
+        K = K.contiguous()
+        V = V.contiguous()
+        out = _C.flash_attention_forward(Q, K, V, bool(causal), float(scale))
+        ctx.save_for_backward(Q, K, V, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        raise NotImplementedError(
+            "Backward pass is not implemented. "
+            "flash-attention-sm75 is for inference only."
+        )
+
+
+def _check_inputs(Q):
+    if Q.dim() != 4:
+        raise ValueError("Q must be 4D [B, H, N, D]")
+    head_dim = Q.size(-1)
+    if head_dim not in (64, 128):
+        raise RuntimeError(
+            f"flash_attention_sm75 supports head_dim=64 or 128, got {head_dim}"
+        )
+    return head_dim
+
+
+def flash_attention_forward(Q, K, V, causal=False, scale=None):
+    """Fused attention forward, drop-in for reference ops.py:55-82.
+
+    Args:
+        Q: [B, H_q,  N, D]  float16, on the GPU
+        K: [B, H_kv, N, D]  float16, H_kv divides H_q
+        V: [B, H_kv, N, D]  float16
+        causal: key j is visible to query i iff j <= i
+        scale: softmax scale (default 1/sqrt(D))
+
+    Returns:
+        O: [B, H_q, N, D] float16
+    """
+    head_dim = _check_inputs(Q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    return FlashAttentionSM75Function.apply(Q, K, V, causal, scale)
+
+
+def flash_attention_forward_lse(Q, K, V, causal=False, scale=None):
+    """Forward that also returns the fp32 row log-sum-exp.
+
+    No reference counterpart (the reference lists LSE as future work).
+    Returns ``(O, LSE)`` with LSE [B, H_q, N] float32, natural log of
+    sum_j exp(scale * q_i . k_j) over the visible keys.
+    """
+    head_dim = _check_inputs(Q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    _check_gqa_heads(Q, K)
+    return _C.flash_attention_forward_lse(
+        Q.contiguous(), K.contiguous(), V.contiguous(), bool(causal), float(scale)
+    )

@@ -1,0 +1,134 @@
+/*
+ * flash_attn_sm75.h -- C ABI of the MI355X (gfx950) fused attention forward.
+ *
+ * Plain pointers and sizes only: no torch, no HIP types in the signatures.
+ * Every tensor is IEEE binary16 (`fa_half`, the bit pattern of CUDA's `half`)
+ * laid out [batch, heads, seq_len, head_dim] with head_dim contiguous.
+ *
+ * Two groups of entry points:
+ *
+ *  1. The four launchers the reference's PyTorch binding declares
+ *     (reference src/bindings/pytorch_extension.cpp:4-19), with the same
+ *     argument order and meaning.  Like the reference launchers they run on
+ *     the default stream and return only after the device is idle; an
+ *     unsupported head_dim prints a message to stderr and returns with O
+ *     untouched (reference src/kernels/flash_attention_forward.cu:812-816).
+ *
+ *  2. The stream-ordered, status-returning entry `fa_sm75_forward`, which
+ *     the Python binding uses.  It adds grouped-query attention (heads_kv
+ *     divides heads_q: query head h reads KV head h / (heads_q / heads_kv),
+ *     the mapping the reference builds with repeat_interleave at
+ *     src/flash_attention_sm75/ops.py:24-26), element strides, an optional
+ *     fp32 row log-sum-exp output, and an explicit hipStream_t.  It
+ *     validates every argument before touching the device and never blocks
+ *     the host.
+ */
+#ifndef FLASH_ATTN_SM75_H
+#define FLASH_ATTN_SM75_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One binary16 value (bit pattern). Only ever passed by pointer. */
+typedef uint16_t fa_half;
+
+/* Status codes returned by fa_sm75_forward / fa_sm75_naive_forward. */
+enum fa_status {
+  FA_OK = 0,
+  FA_ERR_INVALID_ARGUMENT = 1,   /* null pointer, negative size, bad stride */
+  FA_ERR_UNSUPPORTED_HEAD_DIM = 2, /* head_dim not in {64, 128} */
+  FA_ERR_HEADS_NOT_DIVISIBLE = 3,  /* heads_q % heads_kv != 0 */
+  FA_ERR_MISALIGNED = 4,           /* base/row stride not 16-byte aligned */
+  FA_ERR_TOO_LARGE = 5,            /* a grid dimension would overflow */
+  FA_ERR_HIP = 6                   /* HIP runtime error (see message) */
+};
+
+/* Arguments of one forward call.  Strides are in elements; the last
+ * (head_dim) dimension must be contiguous. */
+typedef struct fa_fwd_params {
+  const fa_half* q;  /* [B, Hq,  N, D] */
+  const fa_half* k;  /* [B, Hkv, N, D] */
+  const fa_half* v;  /* [B, Hkv, N, D] */
+  fa_half* o;        /* [B, Hq,  N, D] output */
+  float* lse;        /* optional [B, Hq, N] fp32 natural-log row LSE, or NULL */
+  int64_t batch;
+  int64_t heads_q;
+  int64_t heads_kv;
+  int64_t seq_len;
+  int64_t head_dim;
+  int64_t q_stride_b, q_stride_h, q_stride_n;
+  int64_t k_stride_b, k_stride_h, k_stride_n;
+  int64_t v_stride_b, v_stride_h, v_stride_n;
+  int64_t o_stride_b, o_stride_h, o_stride_n;
+  float scale;       /* softmax scale applied to Q.K (reference default 1/sqrt(D)) */
+  int causal;        /* nonzero: key j is visible to query i iff j <= i */
+  void* stream;      /* hipStream_t; NULL selects the default stream */
+} fa_fwd_params;
+
+/* Fills strides for contiguous [B,H,N,D] tensors. */
+void fa_sm75_set_contiguous_strides(fa_fwd_params* p);
+
+/* Fused MFMA forward.  Replaces the launch in reference
+ * src/kernels/flash_attention_forward.cu:795-817 (and the GQA expansion of
+ * src/flash_attention_sm75/ops.py:6-27).  Asynchronous on p->stream.
+ * Returns FA_OK or an fa_status; fa_sm75_last_error() holds the message. */
+int fa_sm75_forward(const fa_fwd_params* p);
+
+/* Three-pass reference-style path (QK^T -> row softmax -> PV) through an fp32
+ * score workspace of batch*heads_q*seq_len*seq_len floats.  Replaces reference
+ * src/kernels/naive_attention.cu:115-164.  Any head_dim that is a multiple of 8
+ * (1..256) is accepted.  Asynchronous on p->stream. */
+int fa_sm75_naive_forward(const fa_fwd_params* p, float* workspace);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* fa_sm75_last_error(void);
+
+/* Human-readable name of a status code. */
+const char* fa_sm75_status_string(int status);
+
+/* ABI version of this header (bumped on incompatible changes). */
+int fa_sm75_abi_version(void);
+#define FA_SM75_ABI_VERSION 1
+
+/* ---- Reference launcher signatures ------------------------------------ */
+
+/* reference src/bindings/pytorch_extension.cpp:8-11,
+ * src/kernels/flash_attention_forward.cu:795-817 */
+void launch_flash_attention_forward(const fa_half* Q, const fa_half* K,
+                                    const fa_half* V, fa_half* O, int batch,
+                                    int heads, int seq_len, int head_dim,
+                                    float scale, bool causal);
+
+/* reference src/bindings/pytorch_extension.cpp:12-15,
+ * src/kernels/flash_attention_forward.cu:820-833 (head_dim 64 only) */
+void launch_flash_attention_forward_scalar(const fa_half* Q, const fa_half* K,
+                                           const fa_half* V, fa_half* O,
+                                           int batch, int heads, int seq_len,
+                                           int head_dim, float scale,
+                                           bool causal);
+
+/* reference src/bindings/pytorch_extension.cpp:16-19,
+ * src/kernels/flash_attention_forward.cu:836-849 (head_dim 64 only) */
+void launch_flash_attention_forward_wmma_qk(const fa_half* Q, const fa_half* K,
+                                            const fa_half* V, fa_half* O,
+                                            int batch, int heads, int seq_len,
+                                            int head_dim, float scale,
+                                            bool causal);
+
+/* reference src/bindings/pytorch_extension.cpp:4-7,
+ * src/kernels/naive_attention.cu:115-164; workspace holds
+ * batch*heads*seq_len*seq_len floats. */
+void launch_naive_attention(const fa_half* Q, const fa_half* K,
+                            const fa_half* V, fa_half* O, int batch, int heads,
+                            int seq_len, int head_dim, float scale, bool causal,
+                            float* workspace);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASH_ATTN_SM75_H */

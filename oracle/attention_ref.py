@@ -1,0 +1,227 @@
+"""numpy / torch-CPU restatement of the reference attention math.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py): imported by tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg, never by the product.
+
+Reference anchors
+  attention_reference  -> reference src/reference/attention_ref.py:10-45
+  expand_kv_for_gqa    -> reference src/flash_attention_sm75/ops.py:6-27
+  check_correctness    -> reference src/reference/correctness.py:8-37
+  flops                -> reference benchmarks/benchmark_attention.py:78-82
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def default_scale(head_dim: int) -> float:
+    """1/sqrt(D), reference attention_ref.py:24-25 and ops.py:79-80."""
+    return 1.0 / math.sqrt(head_dim)
+
+
+def expand_kv_for_gqa(Q: np.ndarray, K: np.ndarray, V: np.ndarray):
+    """repeat_interleave of K, V along heads (reference ops.py:6-27).
+
+    Query head h reads KV head h // (Hq // Hkv).
+    """
+    h_q, h_kv = Q.shape[1], K.shape[1]
+    if h_q == h_kv:
+        return K, V
+    if h_kv == 0 or h_q % h_kv != 0:
+        raise RuntimeError(
+            f"GQA expansion: Q heads ({h_q}) not divisible by K/V heads ({h_kv})"
+        )
+    f = h_q // h_kv
+    return np.repeat(K, f, axis=1), np.repeat(V, f, axis=1)
+
+
+def _softmax_rows_f32(S: np.ndarray) -> np.ndarray:
+    """torch.softmax(S, dim=-1) in fp32: exp(S - rowmax) / rowsum."""
+    m = S.max(axis=-1, keepdims=True)
+    E = np.exp(S - m, dtype=np.float32)
+    return E / E.sum(axis=-1, keepdims=True, dtype=np.float32)
+
+
+def attention_reference(Q, K, V, causal=False, scale=None, return_f32=False):
+    """The reference's math path, restated (attention_ref.py:10-45).
+
+    fp16 [B,H,N,D] inputs -> fp32 upcast (:28-30) -> S = Q K^T * scale (:32)
+    -> causal triu(diagonal=1) set to -inf (:34-40) -> softmax(dim=-1) (:42)
+    -> P V (:43) -> fp16 (:45).  K, V with fewer heads are expanded first, as
+    the reference API does before calling the kernel (ops.py:35-36).
+    Materialises [B,H,N,N]; use :func:`attention_reference_chunked` for large
+    shapes.
+    """
+    Q = np.asarray(Q)
+    K, V = expand_kv_for_gqa(Q, np.asarray(K), np.asarray(V))
+    if scale is None:
+        scale = default_scale(Q.shape[-1])
+    qf = Q.astype(np.float32)
+    kf = K.astype(np.float32)
+    vf = V.astype(np.float32)
+    S = np.matmul(qf, np.swapaxes(kf, -1, -2)) * np.float32(scale)
+    if causal:
+        n = Q.shape[-2]
+        mask = np.triu(np.ones((n, n), dtype=bool), k=1)
+        S[..., mask] = -np.inf
+    P = _softmax_rows_f32(S)
+    O = np.matmul(P, vf)
+    return O if return_f32 else O.astype(np.float16)
+
+
+def attention_reference_chunked(Q, K, V, causal=False, scale=None, rows=512,
+                                heads=None, return_f32=False):
+    """Same math as :func:`attention_reference`, one (b, h, row block) at a time.
+
+    Rows of the softmax are independent, so evaluating [rows, N] blocks of S
+    gives the same values as the full [N, N] matrix (up to fp32 summation
+    order inside BLAS).  ``heads`` restricts the computation to a list of
+    query-head indices (output has only those heads), which the CPU baseline
+    uses to time a bounded sample.
+    """
+    Q = np.asarray(Q)
+    K = np.asarray(K)
+    V = np.asarray(V)
+    B, Hq, N, D = Q.shape
+    Hkv = K.shape[1]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise RuntimeError(
+            f"GQA expansion: Q heads ({Hq}) not divisible by K/V heads ({Hkv})"
+        )
+    group = Hq // Hkv
+    if scale is None:
+        scale = default_scale(D)
+    hs = list(range(Hq)) if heads is None else list(heads)
+    out = np.empty((B, len(hs), N, D), dtype=np.float32 if return_f32 else np.float16)
+    sc = np.float32(scale)
+    for b in range(B):
+        for oi, h in enumerate(hs):
+            kf = K[b, h // group].astype(np.float32)
+            vf = V[b, h // group].astype(np.float32)
+            kt = np.ascontiguousarray(kf.T)
+            for r0 in range(0, N, rows):
+                r1 = min(N, r0 + rows)
+                qf = Q[b, h, r0:r1].astype(np.float32)
+                S = (qf @ kt) * sc
+                if causal:
+                    cols = np.arange(N)[None, :]
+                    rws = np.arange(r0, r1)[:, None]
+                    S[cols > rws] = -np.inf
+                P = _softmax_rows_f32(S)
+                o = P @ vf
+                out[b, oi, r0:r1] = o if return_f32 else o.astype(np.float16)
+    return out
+
+
+def attention_lse(Q, K, causal=False, scale=None, dtype=np.float64):
+    """Row log-sum-exp: LSE_i = log sum_{j visible} exp(scale * q_i . k_j).
+
+    No reference counterpart (the reference names LSE only as future work);
+    this is the closed form the kernel's optional LSE output must equal.
+    """
+    Q = np.asarray(Q)
+    K = np.asarray(K)
+    B, Hq, N, D = Q.shape
+    group = Hq // K.shape[1]
+    if scale is None:
+        scale = default_scale(D)
+    out = np.empty((B, Hq, N), dtype=dtype)
+    for b in range(B):
+        for h in range(Hq):
+            q = Q[b, h].astype(dtype)
+            k = K[b, h // group].astype(dtype)
+            S = (q @ k.T) * dtype(scale)
+            if causal:
+                S[np.triu(np.ones((N, N), dtype=bool), k=1)] = -np.inf
+            m = S.max(axis=-1, keepdims=True)
+            out[b, h] = (m[:, 0] + np.log(np.exp(S - m).sum(axis=-1)))
+    return out
+
+
+def attention_f64(Q, K, V, causal=False, scale=None):
+    """Brute-force float64 attention (two-pass softmax), for pinning the fp32 path."""
+    Q = np.asarray(Q)
+    K, V = expand_kv_for_gqa(Q, np.asarray(K), np.asarray(V))
+    if scale is None:
+        scale = default_scale(Q.shape[-1])
+    q = Q.astype(np.float64)
+    k = K.astype(np.float64)
+    v = V.astype(np.float64)
+    S = np.matmul(q, np.swapaxes(k, -1, -2)) * float(scale)
+    if causal:
+        n = Q.shape[-2]
+        S[..., np.triu(np.ones((n, n), dtype=bool), k=1)] = -np.inf
+    m = S.max(axis=-1, keepdims=True)
+    E = np.exp(S - m)
+    P = E / E.sum(axis=-1, keepdims=True)
+    return np.matmul(P, v)
+
+
+def check_correctness(output, reference, name="", atol=1e-2, rtol=1e-2):
+    """Error metrics of reference correctness.py:8-37 (numpy restatement).
+
+    max/mean abs error, max/mean relative error abs/(|ref|+1e-8), and
+    allclose semantics |out - ref| <= atol + rtol*|ref| elementwise.
+    """
+    o = np.asarray(output, dtype=np.float32)
+    r = np.asarray(reference, dtype=np.float32)
+    if o.shape != r.shape:
+        raise ValueError(f"shape mismatch {o.shape} vs {r.shape}")
+    abs_err = np.abs(o - r)
+    rel_err = abs_err / (np.abs(r) + np.float32(1e-8))
+    finite = bool(np.isfinite(o).all())
+    is_close = finite and bool(np.all(abs_err <= atol + rtol * np.abs(r)))
+    if o.size == 0:
+        return {"name": name, "max_abs_err": 0.0, "mean_abs_err": 0.0,
+                "max_rel_err": 0.0, "mean_rel_err": 0.0, "allclose": True,
+                "atol": atol, "rtol": rtol}
+    return {
+        "name": name,
+        "max_abs_err": float(abs_err.max()),
+        "mean_abs_err": float(abs_err.mean()),
+        "max_rel_err": float(rel_err.max()),
+        "mean_rel_err": float(rel_err.mean()),
+        "allclose": is_close,
+        "atol": atol,
+        "rtol": rtol,
+    }
+
+
+def flops(batch, heads, seq_len, head_dim, causal=False):
+    """Algorithmic FLOPs 4*B*H*N^2*D, halved for causal
+    (reference benchmarks/benchmark_attention.py:78-82)."""
+    f = 4 * batch * heads * seq_len * seq_len * head_dim
+    return f // 2 if causal else f
+
+
+# ---------------------------------------------------------------------------
+# torch-CPU restatement: the reference's CPU PyTorch path, used as the timed
+# CPU baseline (same ops as attention_ref.py:28-45, evaluated per (b, h) and
+# row block so the [N, N] score matrix fits in host memory).
+# ---------------------------------------------------------------------------
+def attention_reference_torch_cpu(Q, K, V, causal=False, scale=None, rows=2048, heads=None):
+    import torch
+
+    B, Hq, N, D = Q.shape
+    Hkv = K.shape[1]
+    group = Hq // Hkv
+    if scale is None:
+        scale = default_scale(D)
+    hs = list(range(Hq)) if heads is None else list(heads)
+    out = torch.empty((B, len(hs), N, D), dtype=torch.float16)
+    for b in range(B):
+        for oi, h in enumerate(hs):
+            k_f = K[b, h // group].float()
+            v_f = V[b, h // group].float()
+            for r0 in range(0, N, rows):
+                r1 = min(N, r0 + rows)
+                q_f = Q[b, h, r0:r1].float()
+                S = torch.matmul(q_f, k_f.transpose(-2, -1)) * scale
+                if causal:
+                    mask = torch.ones(r1 - r0, N, dtype=torch.bool).triu(diagonal=1 + r0)
+                    S.masked_fill_(mask, float("-inf"))
+                P = torch.softmax(S, dim=-1)
+                out[b, oi, r0:r1] = torch.matmul(P, v_f).half()
+    return out

@@ -1,0 +1,114 @@
+"""The C-ABI library loads and exports every function include/*.h declares.
+
+Calls made here never reach the device: they exercise argument validation,
+which runs before the first HIP call.
+"""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from capi_types import LIB, REPO, Params
+
+
+def declared_functions():
+    names = []
+    for hdr in glob.glob(os.path.join(REPO, "include", "*.h")):
+        text = open(hdr).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b([a-z_][a-z0-9_]*)\s*\(", text):
+            name = m.group(1)
+            prefix = text[:m.start()].rstrip()
+            if name in {"sizeof", "if", "return"}:
+                continue
+            # a declaration: preceded by a type, ends with ');'
+            tail = text[m.end():text.find(";", m.end()) + 1]
+            if tail.endswith(");") and re.search(r"(void|int|char\s*\*|char)\s*\**$", prefix):
+                names.append(name)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(LIB)
+    lib.fa_sm75_forward.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_forward.restype = ctypes.c_int
+    lib.fa_sm75_naive_forward.argtypes = [ctypes.POINTER(Params), ctypes.c_void_p]
+    lib.fa_sm75_naive_forward.restype = ctypes.c_int
+    lib.fa_sm75_last_error.restype = ctypes.c_char_p
+    lib.fa_sm75_status_string.restype = ctypes.c_char_p
+    lib.fa_sm75_set_contiguous_strides.argtypes = [ctypes.POINTER(Params)]
+    return lib
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for n in ("fa_sm75_forward", "fa_sm75_naive_forward", "fa_sm75_last_error",
+              "fa_sm75_status_string", "fa_sm75_abi_version", "fa_sm75_set_contiguous_strides",
+              "launch_flash_attention_forward", "launch_flash_attention_forward_scalar",
+              "launch_flash_attention_forward_wmma_qk", "launch_naive_attention"):
+        assert n in names, n
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+
+
+def make(lib, **kw):
+    p = Params()
+    p.batch, p.heads_q, p.heads_kv, p.seq_len, p.head_dim = 1, 4, 2, 64, 128
+    lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+    p.q = p.k = p.v = p.o = 0x10000
+    p.scale = 0.125
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_contiguous_strides(lib):
+    p = make(lib)
+    assert (p.q_stride_n, p.q_stride_h, p.q_stride_b) == (128, 64 * 128, 4 * 64 * 128)
+    assert (p.k_stride_n, p.k_stride_h, p.k_stride_b) == (128, 64 * 128, 2 * 64 * 128)
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(head_dim=96), 2, b"supports head_dim=64 or 128, got 96"),
+    (dict(heads_kv=3), 3, b"not divisible"),
+    (dict(heads_kv=0), 3, b"heads_kv must be positive"),
+    (dict(seq_len=-1), 1, b"non-negative"),
+    (dict(q=0), 1, b"must not be NULL"),
+    (dict(k=0x10008), 4, b"16-byte aligned"),
+    (dict(q_stride_n=100), 4, b"multiples of 8"),
+    (dict(scale=float("inf")), 1, b"finite"),
+])
+def test_validation_errors(lib, kw, status, msg):
+    p = make(lib, **kw)
+    assert lib.fa_sm75_forward(ctypes.byref(p)) == status
+    assert msg in lib.fa_sm75_last_error()
+    assert lib.fa_sm75_status_string(status) != b"unknown status"
+
+
+def test_null_params(lib):
+    assert lib.fa_sm75_forward(None) == 1
+
+
+def test_empty_problem_is_a_noop(lib):
+    for kw in (dict(batch=0), dict(seq_len=0), dict(heads_q=0)):
+        p = make(lib, q=0, k=0, v=0, o=0, **kw)
+        assert lib.fa_sm75_forward(ctypes.byref(p)) == 0
+
+
+def test_naive_validation(lib):
+    p = make(lib, head_dim=96)
+    p2 = make(lib, head_dim=100)
+    assert lib.fa_sm75_naive_forward(ctypes.byref(p), None) == 1  # workspace NULL
+    assert lib.fa_sm75_naive_forward(ctypes.byref(p2), None) == 2  # not a multiple of 8
+
+
+def test_abi_version(lib):
+    assert lib.fa_sm75_abi_version() == 1
