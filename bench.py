@@ -161,6 +161,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--all", action="store_true", help="also time C1..C5 (stderr)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain elementwise copy of 256 MiB (known HBM bytes) "
+                         "to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -173,6 +176,16 @@ def main():
     cfg = args.config
     B, Hq, Hkv, N, D, causal, _, _ = CONFIGS[cfg]
     F = flops(B, Hq, N, D, causal)
+
+    if args.copy_calibration:
+        n = 128 * 1024 * 1024  # fp16 elements: 256 MiB read + 256 MiB written
+        src = torch.ones(n, dtype=torch.float16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"[copy-calibration] 3 launches of torch.mul over {2 * n} bytes in, {2 * n} bytes out")
+        del src, dst
 
     if args.all:
         for c in sorted(CONFIGS):
