@@ -79,6 +79,10 @@ int validate(const fa_fwd_params* p, bool fused) {
   if (p->seq_len > (int64_t)fa::fused_block_m() * 65535 || p->seq_len > INT32_MAX / 2)
     return fail(FA_ERR_TOO_LARGE, "seq_len %lld exceeds the supported maximum",
                 (long long)p->seq_len);
+  // K/V tiles are read through 32-bit buffer windows over one (batch, head).
+  if (p->seq_len * p->k_stride_n * 2 > (int64_t)INT32_MAX ||
+      p->seq_len * p->v_stride_n * 2 > (int64_t)INT32_MAX)
+    return fail(FA_ERR_TOO_LARGE, "seq_len * row stride of K/V exceeds 2^31 bytes");
   if (p->batch * p->heads_q > (int64_t)(1u << 24))
     return fail(FA_ERR_TOO_LARGE, "batch*heads_q %lld exceeds 2^24",
                 (long long)(p->batch * p->heads_q));

@@ -8,7 +8,8 @@
 //   grid.x = batch * heads_q, grid.y = query blocks of kBlockM = 128 rows.
 //   One workgroup = 4 waves; wave w owns query rows [q0 + 32w, q0 + 32w + 32).
 //   Key/value rows stream through LDS in tiles of kBlockN = 64 keys, double
-//   buffered (global -> VGPR staging -> LDS), one barrier per tile.
+//   buffered (buffer loads -> VGPR staging -> LDS), one barrier per tile.  The
+//   buffer windows end at the last key, so rows past the sequence read as 0.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_f16, operand layouts verified on the
 // device):
@@ -45,33 +46,37 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBlockM = 32 * kWaves;  // queries per workgroup
 constexpr int kBlockN = 64;           // keys per LDS tile
+// Online-softmax rescale threshold (log2 units): the running max used for
+// the exponent is only raised when a row's tile max exceeds it by more than
+// this, so P stays <= 2^8 and the O/l rescale is skipped for most tiles.
+// The result is mathematically unchanged (l and O use the same stale max).
+constexpr float kRescaleLog2 = 8.0f;
 
-// XOR swizzle of the 16-byte chunk index inside an LDS row, as a function of
-// the row.  For D = 128 (16 chunks / 256 B per row) it makes
-//  * the K-operand reads (32 rows x one 16 B chunk) hit 16 distinct chunk
-//    slots per 16 lanes, and
-//  * the transposing V reads (4 consecutive rows x one 32 B chunk pair per
-//    16 lanes) hit 4 distinct pair slots.
-// For D = 64 (8 chunks / 128 B per row, two rows per 256 B bank sweep) the
-// same two properties hold with the rows' parity taken into account.
+// LDS tile layout: row r of a K or V tile starts at r * Pitch halves, with
+// Pitch = D + 32 (64 bytes of padding per row), and its 16-byte chunk c is
+// stored at chunk position c ^ ((r >> 2) & 3).  The padding shifts each row
+// by 64 bytes modulo the 256-byte bank sweep, the XOR spreads the 4 rows of
+// each aligned group over the 4 chunks of a 64-byte block.  Together:
+//  * K operand reads (ds_read_b128, 16 lanes = 16 consecutive rows, one
+//    chunk) hit 16 distinct 16-byte bank groups;
+//  * transposing V reads (ds_read_b64_tr_b16, 32 lanes = 4 rows x two
+//    32-byte chunk pairs) hit 8 distinct pair slots;
+//  * the XOR only touches the low two chunk bits, so every address is a
+//    per-lane base plus a compile-time immediate.
 template <int D>
-__device__ __forceinline__ int chunk_swizzle(int row) {
-  if constexpr (D == 128) {
-    return ((row & 7) << 1) | ((row >> 3) & 1);
-  } else {
-    return (((row >> 1) & 3) << 1) | ((row >> 3) & 1);
+struct Lds {
+  static constexpr int Pitch = D + 32;          // halves per row
+  static constexpr int Tile = kBlockN * Pitch;  // halves per K (or V) tile
+  __device__ static __forceinline__ int at(int row, int chunk) {
+    return row * Pitch + 8 * (chunk ^ ((row >> 2) & 3));
   }
-}
-
-template <int D>
-__device__ __forceinline__ int lds_offset(int row, int chunk) {
-  return row * D + 8 * (chunk ^ chunk_swizzle<D>(row));
-}
+};
 
 __device__ __forceinline__ half4 ds_read_tr16(const _Float16* p) {
   short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -79,28 +84,54 @@ __device__ __forceinline__ half4 ds_read_tr16(const _Float16* p) {
   return __builtin_bit_cast(half4, r);
 }
 
-__device__ __forceinline__ float xor32(float x) {
-  const int lane = __lane_id();
-  int r = __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, x));
-  return __builtin_bit_cast(float, r);
+// Combines the two half-wave copies of a per-query value (lanes l and l^32):
+// v_permlane32_swap(x, x) yields [x_lo, x_lo] and [x_hi, x_hi].
+__device__ __forceinline__ float halves_max(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
+// Raw buffer resource over [base, base + bytes): loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes,
+                                           0x00020000);
+}
+
+template <bool B>
+struct Flag {
+  static constexpr bool value = B;
+};
+
+// Software-pipelined main loop: iteration j computes S^T_{j+1} = K_{j+1} Q^T
+// on the MFMA pipe while the VALU turns S^T_j into probabilities, then
+// accumulates P_j V_j.  LDS holds two K and two V tiles; during iteration j
+// the loads of K_{j+2} and V_{j+1} land in the buffers freed by iteration
+// j-1, so one barrier per iteration suffices.
 template <int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
+  using L = Lds<D>;
   constexpr int KK = D / 16;      // 16-wide contraction steps of S^T
   constexpr int MT = D / 32;      // 32-row output tiles of O^T
   constexpr int CPR = D / 8;      // 16-byte chunks per K/V row
-  constexpr int TILE = kBlockN * D;
   constexpr int LOADS = kBlockN * CPR / kThreads;  // chunks per thread per tile
   static_assert(LOADS * kThreads == kBlockN * CPR, "tile must split evenly");
 
-  __shared__ __attribute__((aligned(16))) _Float16 smem[4 * TILE];
+  // [K buffer 0 | K buffer 1 | V buffer 0 | V buffer 1]
+  __shared__ __attribute__((aligned(16))) _Float16 smem[4 * L::Tile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int hi = lane >> 5;   // which half of the wave
   const int ql = lane & 31;   // query column owned by this lane
+  const int grp = lane >> 4;  // 16-lane group (transposing reads)
+  const int gi = lane & 15;
 
   const int bh = blockIdx.x;
   const int b = bh / a.hq;
@@ -134,34 +165,70 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const int kv_len = CAUSAL ? min(N, q0 + kBlockM) : N;
   const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
 
+  // Per-lane constants of the tile loader: global byte offset inside a tile
+  // and LDS position of each of the LOADS chunks this lane moves.
+  int g_off_k[LOADS], g_off_v[LOADS], l_off[LOADS];
+#pragma unroll
+  for (int p = 0; p < LOADS; ++p) {
+    const int g = p * kThreads + tid;
+    const int row = g / CPR;
+    const int c = g % CPR;
+    g_off_k[p] = (int)(row * a.ksn * 2) + 16 * c;
+    g_off_v[p] = (int)(row * a.vsn * 2) + 16 * c;
+    l_off[p] = L::at(row, c);
+  }
+  const int k_tile_bytes = (int)(kBlockN * a.ksn * 2);
+  const int v_tile_bytes = (int)(kBlockN * a.vsn * 2);
+  const int k_all_bytes = (int)(N * a.ksn * 2);
+  const int v_all_bytes = (int)(N * a.vsn * 2);
+
+  // Resource windows start at the tile; rows >= N fall past the end and read
+  // as zero, so the sequence tail needs no branch.
   u32x4 kst[LOADS], vst[LOADS];
-  auto load_tile = [&](int j) {
+  auto load_k = [&](int j) {
+    const __amdgpu_buffer_rsrc_t r =
+        make_rsrc(Kp + (int64_t)j * kBlockN * a.ksn, k_all_bytes - j * k_tile_bytes);
 #pragma unroll
-    for (int p = 0; p < LOADS; ++p) {
-      const int g = p * kThreads + tid;
-      const int row = g / CPR;
-      const int c = g % CPR;
-      const int key = j * kBlockN + row;
-      if (key < N) {
-        kst[p] = *(const u32x4*)(Kp + (int64_t)key * a.ksn + 8 * c);
-        vst[p] = *(const u32x4*)(Vp + (int64_t)key * a.vsn + 8 * c);
-      } else {
-        kst[p] = (u32x4)0u;
-        vst[p] = (u32x4)0u;
-      }
-    }
+    for (int p = 0; p < LOADS; ++p) kst[p] = __builtin_amdgcn_raw_buffer_load_b128(r, g_off_k[p], 0, 0);
   };
-  auto store_tile = [&](int buf) {
-    _Float16* Ks = smem + buf * 2 * TILE;
-    _Float16* Vs = Ks + TILE;
+  auto load_v = [&](int j) {
+    const __amdgpu_buffer_rsrc_t r =
+        make_rsrc(Vp + (int64_t)j * kBlockN * a.vsn, v_all_bytes - j * v_tile_bytes);
 #pragma unroll
-    for (int p = 0; p < LOADS; ++p) {
-      const int g = p * kThreads + tid;
-      const int row = g / CPR;
-      const int c = g % CPR;
-      const int off = lds_offset<D>(row, c);
-      *(u32x4*)(Ks + off) = kst[p];
-      *(u32x4*)(Vs + off) = vst[p];
+    for (int p = 0; p < LOADS; ++p) vst[p] = __builtin_amdgcn_raw_buffer_load_b128(r, g_off_v[p], 0, 0);
+  };
+  auto store_k = [&](int buf) {
+    _Float16* dst = smem + buf * L::Tile;
+#pragma unroll
+    for (int p = 0; p < LOADS; ++p) *(u32x4*)(dst + l_off[p]) = kst[p];
+  };
+  auto store_v = [&](int buf) {
+    _Float16* dst = smem + (2 + buf) * L::Tile;
+#pragma unroll
+    for (int p = 0; p < LOADS; ++p) *(u32x4*)(dst + l_off[p]) = vst[p];
+  };
+
+  // Per-lane LDS bases of the operand reads (see Lds): K rows ql (+32t),
+  // chunk 2kk + hi; V rows 16ks + 4hi + gi/4 (+8), dims 32mt + 16(grp&1) + 4(gi&3).
+  const int sK = (ql >> 2) & 3;
+  const int k_base_even = ql * L::Pitch + 8 * (hi ^ sK);
+  const int k_base_odd = ql * L::Pitch + 8 * ((2 + hi) ^ sK);
+  const int v_row = 4 * hi + (gi >> 2);
+  const int v_c = 2 * (grp & 1) + ((gi & 3) >> 1);
+  const int v_base0 = v_row * L::Pitch + 8 * (v_c ^ hi) + 4 * (gi & 1);
+  const int v_base1 = (v_row + 8) * L::Pitch + 8 * (v_c ^ (hi + 2)) + 4 * (gi & 1);
+
+  // S^T = K Q^T for the 64 keys of one LDS K buffer: two 32-key sub-tiles.
+  auto qk = [&](const _Float16* Ks, float16v (&s)[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = (float16v)0.0f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const int off = ((kk & 1) ? k_base_odd : k_base_even) + 32 * t * L::Pitch + 32 * (kk >> 1);
+        const half8 kf = *(const half8*)(Ks + off);
+        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], s[t], 0, 0, 0);
+      }
     }
   };
 
@@ -171,108 +238,123 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   float m_run = -__builtin_inff();
   float l_run = 0.0f;
   const float c2 = a.c;  // |scale| * log2(e)
+  const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
+  float16v s_cur[2], s_nxt[2];
 
-  for (int j = 0; j < ntiles; ++j) {
-    const int buf = j & 1;
-    const bool has_next = (j + 1) < ntiles;
-    if (has_next) load_tile(j + 1);
+  // One pipeline step for tile j (HAS_NEXT: tile j+1 exists, so S_{j+1} is
+  // computed here and tile j+1's V / tile j+2's K are staged).
+  auto step = [&](int j, auto has_next_t) {
+    constexpr bool HAS_NEXT = decltype(has_next_t)::value;
+    const bool more2 = (j + 2) < ntiles;
+    if (HAS_NEXT) {
+      if (more2) load_k(j + 2);
+      load_v(j + 1);
+    }
 
+    // ---- mask (sequence tail, causal diagonal) --------------------------
     const int kstart = j * kBlockN;
-    const bool active = !CAUSAL || (kstart <= qw + 31);
-    if (active) {
-      const _Float16* Ks = smem + buf * 2 * TILE;
-      const _Float16* Vs = Ks + TILE;
-
-      // ---- S^T = K Q^T : two 32-key sub-tiles -------------------------------
-      float16v s[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        s[t] = (float16v)0.0f;
-        const int row = 32 * t + ql;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          const half8 kf = *(const half8*)(Ks + lds_offset<D>(row, 2 * kk + hi));
-          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], s[t], 0, 0, 0);
-        }
-      }
-
-      // ---- mask (sequence tail, causal diagonal) ----------------------------
-      const bool need_mask = (kstart + kBlockN > N) || (CAUSAL && kstart + kBlockN - 1 > qw);
-      if (need_mask) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
-            const bool masked = (key >= N) || (CAUSAL && key > qrow);
-            if (masked) s[t][i] = -__builtin_inff();
-          }
-        }
-      }
-
-      // ---- online softmax on the accumulator layout -------------------------
-      float mx = s[0][0];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[t][i]);
-      }
-      mx = fmaxf(mx, xor32(mx));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
-      const float alpha =
-          (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * c2);
-      const float mc = m_use * c2;
-
-      half8 pf[4];
-      float lsum = 0.0f;
+    const bool need_mask = (kstart + kBlockN > N) || (CAUSAL && kstart + kBlockN - 1 > qw);
+    if (need_mask) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], c2, -mc));
-          lsum += p;
-          pf[2 * t + (i >> 3)][i & 7] = (_Float16)p;
-        }
-      }
-      l_run = l_run * alpha + lsum;
-      m_run = m_new;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) oacc[mt] *= alpha;
-
-      // ---- O^T += V^T P^T ---------------------------------------------------
-      // Key order of 16-key step ks (sub-tile t = ks/2, half s = ks%2):
-      // element e of the lane's 8 = key 32t + 16s + 8(e/4) + 4*hi + e%4.
-      const int grp = lane >> 4;   // 16-lane group
-      const int gi = lane & 15;    // index inside the group
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int rbase = 16 * ks + 4 * hi + (gi >> 2);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int d = 32 * mt + 16 * (grp & 1) + 4 * (gi & 3);
-          const int chunk = d >> 3;
-          const int sub = d & 7;
-          const half4 lo = ds_read_tr16(Vs + lds_offset<D>(rbase, chunk) + sub);
-          const half4 hi4 = ds_read_tr16(Vs + lds_offset<D>(rbase + 8, chunk) + sub);
-          const half8 vf = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-          oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], oacc[mt], 0, 0, 0);
+          const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
+          const bool masked = (key >= N) || (CAUSAL && key > qrow);
+          if (masked) s_cur[t][i] = -__builtin_inff();
         }
       }
     }
 
-    if (has_next) store_tile(buf ^ 1);
-    __syncthreads();
+    // ---- running max; raise it only when some row outgrew it by 2^8 -----
+    float mx = s_cur[0][0];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[t][i]);
+    }
+    mx = halves_max(mx);
+    const bool grow = (mx - m_run) * c2 > kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
+      const float alpha =
+          (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) oacc[mt] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = ((m_run == -__builtin_inff()) ? 0.0f : m_run) * c2;
+
+    // ---- S_{j+1} on the MFMA pipe, P_j on the VALU -----------------------
+    if (HAS_NEXT) qk(smem + ((j + 1) & 1) * L::Tile, s_nxt);
+
+    half8 pf[4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i], c2, -mc));
+        pf[2 * t + (i >> 3)][i & 7] = (_Float16)p;
+      }
+    }
+    // Row sum of the fp16 probabilities actually used in P V.
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const half2v pr = {pf[ks][2 * e], pf[ks][2 * e + 1]};
+        l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
+      }
+    }
+
+    // ---- O^T += V_j^T P_j^T -----------------------------------------------
+    // Key order of 16-key step ks (sub-tile t = ks/2, half s = ks%2):
+    // element e of the lane's 8 = key 32t + 16s + 8(e/4) + 4*hi + e%4.
+    const _Float16* Vs = smem + (2 + (j & 1)) * L::Tile;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int imm = 16 * ks * L::Pitch + 32 * mt;
+        const half4 lo = ds_read_tr16(Vs + v_base0 + imm);
+        const half4 hi4 = ds_read_tr16(Vs + v_base1 + imm);
+        const half8 vf = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], oacc[mt], 0, 0, 0);
+      }
+    }
+
+    if (HAS_NEXT) {
+      if (more2) store_k(j & 1);
+      store_v((j + 1) & 1);
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < 2; ++t) s_cur[t] = s_nxt[t];
+    }
+  };
+
+  // ---- prologue: K_0, V_0, K_1 into LDS; S_0 -------------------------------
+  if (ntiles > 0) {
+    load_k(0);
+    load_v(0);
+    store_k(0);
+    store_v(0);
+    if (ntiles > 1) {
+      load_k(1);
+      store_k(1);
+    }
+  }
+  __syncthreads();
+  if (ntiles > 0) {
+    qk(smem, s_cur);
+    for (int j = 0; j + 1 < ntiles; ++j) step(j, Flag<true>{});
+    step(ntiles - 1, Flag<false>{});
   }
 
   // ---- epilogue: combine the two half-wave partial sums, normalise, store ---
-  const float l_tot = l_run + xor32(l_run);
+  const float l_tot = halves_sum(l_run);
   const float inv = (l_tot > 0.0f) ? (1.0f / l_tot) : 0.0f;
   if (qrow < N) {
     _Float16* op = a.o + b * a.osb + hq * a.osh + (int64_t)qrow * a.osn;
