@@ -7,9 +7,10 @@
 // Work decomposition
 //   grid.x = batch * heads_q, grid.y = query blocks of kBlockM = 128 rows.
 //   One workgroup = 4 waves; wave w owns query rows [q0 + 32w, q0 + 32w + 32).
-//   Key/value rows stream through LDS in tiles of kBlockN = 64 keys, double
-//   buffered (buffer loads -> VGPR staging -> LDS), one barrier per tile.  The
-//   buffer windows end at the last key, so rows past the sequence read as 0.
+//   Key/value rows stream through LDS in tiles of kBlockN = 64 keys.  Tiles
+//   go straight from HBM to LDS (buffer_load ... lds: lane l's 16 bytes land
+//   at M0 + 16 l), through buffer windows that end at the last key, so rows
+//   past the sequence arrive as zeros.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_f16, operand layouts verified on the
 // device):
@@ -18,8 +19,8 @@
 //   C[m][n]: lane l holds n = l%32, m = 8*(i/4) + 4*(l/32) + i%4 (16 floats)
 //   * S^T = K Q^T: keys are the M side, queries the N side, so every lane owns
 //     a single query (l%32) and 16 of its 32 keys per 32-key sub-tile.  The
-//     row max over keys is an in-register reduction plus one exchange with
-//     lane l^32; the row sum never needs an exchange until the very end.
+//     row max over keys is an in-register reduction plus one lane swap
+//     between the two wave halves; the row sum stays lane-local until the end.
 //   * O^T = V^T P^T: the probabilities stay in the registers the S^T
 //     accumulator produced, reinterpreted as the B operand.  The key order
 //     inside each 16-key MFMA step is a permutation shared by P and V (the
@@ -27,6 +28,13 @@
 //     row-major LDS tile with ds_read_b64_tr_b16 (transposing LDS read).
 //   * The O^T accumulator keeps, per lane, one query and D/2 of its
 //     dimensions, so the online-softmax rescale is a per-lane scalar.
+//
+// Scheduling.  On this hardware a wave's VALU work overlaps its *own* MFMAs
+// (issued between them) but hardly overlaps MFMAs of another wave on the
+// same SIMD.  So the main loop is software pipelined and hand ordered:
+// iteration j issues the MFMAs of S_{j+1} and P_j V_j one "slot" at a time,
+// and each slot also carries the LDS reads needed a few slots later and a
+// share of the softmax of S_j (exp, fp16 pack, row sum).
 //
 // Softmax numerics follow reference src/kernels/flash_attention_forward.cu:
 // running max starts at -inf and the first rescale factor is 0 (:386,:483),
@@ -43,10 +51,11 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
@@ -69,13 +78,15 @@ constexpr float kRescaleLog2 = 8.0f;
 //    32-byte chunk pairs) hit 8 distinct pair slots;
 //  * the XOR only touches the low two chunk bits, so every address is a
 //    per-lane base plus a compile-time immediate.
+// A tile is written by whole-wave direct loads of 1 KB segments; lanes whose
+// 16 bytes fall in the padding load from past the buffer window (zeros).
 template <int D>
 struct Lds {
-  static constexpr int Pitch = D + 32;          // halves per row
-  static constexpr int Tile = kBlockN * Pitch;  // halves per K (or V) tile
-  __device__ static __forceinline__ int at(int row, int chunk) {
-    return row * Pitch + 8 * (chunk ^ ((row >> 2) & 3));
-  }
+  static constexpr int Pitch = D + 32;           // halves per row
+  static constexpr int Tile = kBlockN * Pitch;   // halves per K (or V) tile
+  static constexpr int Segs = Tile * 2 / 1024;   // 1 KB direct-load segments
+  static constexpr int SegsPerWave = Segs / kWaves;
+  static_assert(Segs % kWaves == 0, "segments must split over the waves");
 };
 
 __device__ __forceinline__ half4 ds_read_tr16(const _Float16* p) {
@@ -103,27 +114,48 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
                                            0x00020000);
 }
 
+// 16 bytes per lane from a buffer window straight into LDS (lane l writes
+// dst + 16 l).  Kept out of line of the kernel template so the host pass
+// still emits the kernel's launch stub.
+__device__ __forceinline__ void direct_load16(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
+}
+
+// Freezes the instruction order at this point (nothing is moved across).
+__device__ __forceinline__ void fence_schedule() { __builtin_amdgcn_sched_barrier(0); }
+
+// Workgroup barrier that also publishes this wave's direct-to-LDS loads:
+// they are counted by vmcnt, which the compiler does not drain before
+// s_barrier on its own.  0x0F70 = vmcnt(0) expcnt(7) lgkmcnt(15) (gfx9).
+__device__ __forceinline__ void barrier_after_direct_loads() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+}
+
 template <bool B>
 struct Flag {
   static constexpr bool value = B;
 };
 
 // Software-pipelined main loop: iteration j computes S^T_{j+1} = K_{j+1} Q^T
-// on the MFMA pipe while the VALU turns S^T_j into probabilities, then
-// accumulates P_j V_j.  LDS holds two K and two V tiles; during iteration j
-// the loads of K_{j+2} and V_{j+1} land in the buffers freed by iteration
-// j-1, so one barrier per iteration suffices.
+// while the VALU turns S^T_j into probabilities, then accumulates P_j V_j.
+// LDS holds two K and two V tiles; the direct loads of K_{j+2} and V_{j+1}
+// issued at the top of iteration j land in the buffers iteration j-1 freed,
+// so one barrier per iteration suffices.
 template <int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   using L = Lds<D>;
-  constexpr int KK = D / 16;      // 16-wide contraction steps of S^T
-  constexpr int MT = D / 32;      // 32-row output tiles of O^T
-  constexpr int CPR = D / 8;      // 16-byte chunks per K/V row
-  constexpr int LOADS = kBlockN * CPR / kThreads;  // chunks per thread per tile
-  static_assert(LOADS * kThreads == kBlockN * CPR, "tile must split evenly");
+  constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
+  constexpr int MT = D / 32;       // 32-row output tiles of O^T
+  constexpr int NS = 2 * KK;       // S^T MFMAs per tile
+  constexpr int NPV = 4 * MT;      // P V MFMAs per tile
+  constexpr int NSA = 4;           // S^T MFMAs issued while the row max is formed
+  constexpr int PFK = 3;           // K operand reads run this many MFMAs ahead
+  constexpr int PFV = 2;           // V operand reads run this many MFMAs ahead
+  constexpr int SEGW = L::SegsPerWave;
 
   // [K buffer 0 | K buffer 1 | V buffer 0 | V buffer 1]
-  __shared__ __attribute__((aligned(16))) _Float16 smem[4 * L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[4 * L::Tile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -165,47 +197,45 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const int kv_len = CAUSAL ? min(N, q0 + kBlockM) : N;
   const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
 
-  // Per-lane constants of the tile loader: global byte offset inside a tile
-  // and LDS position of each of the LOADS chunks this lane moves.
-  int g_off_k[LOADS], g_off_v[LOADS], l_off[LOADS];
+  // Direct-load map: wave w fills 1 KB segments w, w + 4, ...; lane l of a
+  // segment covers tile bytes [1024 seg + 16 l, +16).  Precompute the global
+  // byte offset inside a tile for each segment (padding lanes: past the end).
+  int goff_k[SEGW], goff_v[SEGW];
 #pragma unroll
-  for (int p = 0; p < LOADS; ++p) {
-    const int g = p * kThreads + tid;
-    const int row = g / CPR;
-    const int c = g % CPR;
-    g_off_k[p] = (int)(row * a.ksn * 2) + 16 * c;
-    g_off_v[p] = (int)(row * a.vsn * 2) + 16 * c;
-    l_off[p] = L::at(row, c);
+  for (int s = 0; s < SEGW; ++s) {
+    const int pos = (wave + kWaves * s) * 1024 + 16 * lane;  // bytes into the tile
+    const int row = pos / (2 * L::Pitch);
+    const int within = pos - row * (2 * L::Pitch);
+    if (within < 2 * D) {
+      const int c = (within >> 4) ^ ((row >> 2) & 3);
+      goff_k[s] = (int)(row * a.ksn * 2) + 16 * c;
+      goff_v[s] = (int)(row * a.vsn * 2) + 16 * c;
+    } else {
+      goff_k[s] = -16;  // 0xfffffff0: beyond any window -> writes zeros
+      goff_v[s] = -16;
+    }
   }
   const int k_tile_bytes = (int)(kBlockN * a.ksn * 2);
   const int v_tile_bytes = (int)(kBlockN * a.vsn * 2);
   const int k_all_bytes = (int)(N * a.ksn * 2);
   const int v_all_bytes = (int)(N * a.vsn * 2);
 
-  // Resource windows start at the tile; rows >= N fall past the end and read
-  // as zero, so the sequence tail needs no branch.
-  u32x4 kst[LOADS], vst[LOADS];
-  auto load_k = [&](int j) {
+  auto lds_seg = [&](int tile_index, int s) -> lds_void* {
+    return (lds_void*)(smem + tile_index * L::Tile + (wave + kWaves * s) * 512);
+  };
+  auto load_k = [&](int j, int buf) {
     const __amdgpu_buffer_rsrc_t r =
         make_rsrc(Kp + (int64_t)j * kBlockN * a.ksn, k_all_bytes - j * k_tile_bytes);
 #pragma unroll
-    for (int p = 0; p < LOADS; ++p) kst[p] = __builtin_amdgcn_raw_buffer_load_b128(r, g_off_k[p], 0, 0);
+    for (int s = 0; s < SEGW; ++s)
+      direct_load16(r, lds_seg(buf, s), goff_k[s]);
   };
-  auto load_v = [&](int j) {
+  auto load_v = [&](int j, int buf) {
     const __amdgpu_buffer_rsrc_t r =
         make_rsrc(Vp + (int64_t)j * kBlockN * a.vsn, v_all_bytes - j * v_tile_bytes);
 #pragma unroll
-    for (int p = 0; p < LOADS; ++p) vst[p] = __builtin_amdgcn_raw_buffer_load_b128(r, g_off_v[p], 0, 0);
-  };
-  auto store_k = [&](int buf) {
-    _Float16* dst = smem + buf * L::Tile;
-#pragma unroll
-    for (int p = 0; p < LOADS; ++p) *(u32x4*)(dst + l_off[p]) = kst[p];
-  };
-  auto store_v = [&](int buf) {
-    _Float16* dst = smem + (2 + buf) * L::Tile;
-#pragma unroll
-    for (int p = 0; p < LOADS; ++p) *(u32x4*)(dst + l_off[p]) = vst[p];
+    for (int s = 0; s < SEGW; ++s)
+      direct_load16(r, lds_seg(2 + buf, s), goff_v[s]);
   };
 
   // Per-lane LDS bases of the operand reads (see Lds): K rows ql (+32t),
@@ -218,18 +248,19 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const int v_base0 = v_row * L::Pitch + 8 * (v_c ^ hi) + 4 * (gi & 1);
   const int v_base1 = (v_row + 8) * L::Pitch + 8 * (v_c ^ (hi + 2)) + 4 * (gi & 1);
 
-  // S^T = K Q^T for the 64 keys of one LDS K buffer: two 32-key sub-tiles.
-  auto qk = [&](const _Float16* Ks, float16v (&s)[2]) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      s[t] = (float16v)0.0f;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const int off = ((kk & 1) ? k_base_odd : k_base_even) + 32 * t * L::Pitch + 32 * (kk >> 1);
-        const half8 kf = *(const half8*)(Ks + off);
-        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], s[t], 0, 0, 0);
-      }
-    }
+  // K operand i (sub-tile t = i / KK, step kk = i % KK) of one K buffer.
+  auto read_k = [&](const _Float16* Ks, int i) -> half8 {
+    const int t = i / KK, kk = i % KK;
+    const int off = ((kk & 1) ? k_base_odd : k_base_even) + 32 * t * L::Pitch + 32 * (kk >> 1);
+    return *(const half8*)(Ks + off);
+  };
+  // V^T operand v (16-key step ks = v / MT, output tile mt = v % MT).
+  auto read_v = [&](const _Float16* Vs, int v) -> half8 {
+    const int ks = v / MT, mt = v % MT;
+    const int imm = 16 * ks * L::Pitch + 32 * mt;
+    const half4 lo = ds_read_tr16(Vs + v_base0 + imm);
+    const half4 hi4 = ds_read_tr16(Vs + v_base1 + imm);
+    return __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
   float16v oacc[MT];
@@ -242,14 +273,18 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
 
   float16v s_cur[2], s_nxt[2];
 
-  // One pipeline step for tile j (HAS_NEXT: tile j+1 exists, so S_{j+1} is
-  // computed here and tile j+1's V / tile j+2's K are staged).
+  // One pipeline step for tile j.  HAS_NEXT: tile j+1 exists, so S_{j+1} is
+  // computed here and the loads of V_{j+1} (and K_{j+2}) are issued.
   auto step = [&](int j, auto has_next_t) {
     constexpr bool HAS_NEXT = decltype(has_next_t)::value;
-    const bool more2 = (j + 2) < ntiles;
+    constexpr int ns = HAS_NEXT ? NS : 0;     // S MFMAs this step
+    constexpr int nsa = HAS_NEXT ? NSA : 0;   // ... of which in the max block
+    const _Float16* Kn = smem + ((j + 1) & 1) * L::Tile;
+    const _Float16* Vc = smem + (2 + (j & 1)) * L::Tile;
+
     if (HAS_NEXT) {
-      if (more2) load_k(j + 2);
-      load_v(j + 1);
+      if (j + 2 < ntiles) load_k(j + 2, j & 1);
+      load_v(j + 1, (j + 1) & 1);
     }
 
     // ---- mask (sequence tail, causal diagonal) --------------------------
@@ -267,14 +302,29 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
       }
     }
 
-    // ---- running max; raise it only when some row outgrew it by 2^8 -----
-    float mx = s_cur[0][0];
+    // ---- block A: first S_{j+1} MFMAs while the row max is formed --------
+    half8 kf[NS > 0 ? NS : 1];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int i = 0; i < PFK && i < ns; ++i) kf[i] = read_k(Kn, i);
+    float mx = -__builtin_inff();
+    constexpr int MAXA = nsa > 0 ? nsa : 1;   // slots the max is spread over
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[t][i]);
+    for (int slot = 0; slot < MAXA; ++slot) {
+      if (slot < nsa) {
+        const int i = slot;
+        if (i + PFK < ns) kf[i + PFK] = read_k(Kn, i + PFK);
+        const int t = i / KK, kk = i % KK;
+        s_nxt[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            kf[i], qf[kk], kk == 0 ? (float16v)0.0f : s_nxt[t], 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = slot * 32 / MAXA; e < (slot + 1) * 32 / MAXA; ++e)
+        mx = fmaxf(mx, s_cur[e >> 4][e & 15]);
+      fence_schedule();
     }
     mx = halves_max(mx);
+
+    // ---- raise the running max only when some row outgrew it by 2^8 -----
     const bool grow = (mx - m_run) * c2 > kRescaleLog2;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
       const float m_new = fmaxf(m_run, mx);
@@ -288,48 +338,69 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
     }
     const float mc = ((m_run == -__builtin_inff()) ? 0.0f : m_run) * c2;
 
-    // ---- S_{j+1} on the MFMA pipe, P_j on the VALU -----------------------
-    if (HAS_NEXT) qk(smem + ((j + 1) & 1) * L::Tile, s_nxt);
-
+    // ---- block B: remaining S_{j+1} MFMAs, then P_j V_j; the softmax of --
+    // S_j (16 pairs of scores) is spread over the slots.  Within a slot the
+    // MFMA is issued first, so the pairs of 16-key step ks must sit in a
+    // slot before the first P V MFMA of step ks; pairs that cannot (the
+    // last tile has no S MFMAs to hide them behind) go before the loop.
+    constexpr int NB = (ns - nsa) + NPV;            // MFMA slots in block B
+    constexpr int PV_FIRST = ns - nsa;              // slot of the first P V MFMA
+    constexpr int PAIR_SLOTS = NB - MT;             // slots available to pairs
     half8 pf[4];
+    half8 vf[NPV];
+    auto pair_slot = [&](int p) {
+      const int spread = (p * PAIR_SLOTS) / 16;
+      const int last_ok = PV_FIRST + (p / 4) * MT - 1;
+      return spread < last_ok ? spread : last_ok;
+    };
+    auto softmax_pair = [&](int p) {
+      const int e = 2 * p;
+      const int t = e >> 4, i = e & 15;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i], c2, -mc));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i + 1], c2, -mc));
+      const half2v pr = {(_Float16)p0, (_Float16)p1};
+      pf[2 * t + (i >> 3)][i & 7] = pr[0];
+      pf[2 * t + (i >> 3)][(i & 7) + 1] = pr[1];
+      l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
+    };
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i], c2, -mc));
-        pf[2 * t + (i >> 3)][i & 7] = (_Float16)p;
-      }
+    for (int p = 0; p < 16; ++p) {
+      if (pair_slot(p) < 0) softmax_pair(p);
     }
-    // Row sum of the fp16 probabilities actually used in P V.
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int slot = 0; slot < NB; ++slot) {
+      const int pv_first = PV_FIRST;
+      // V operand reads, PFV MFMAs ahead of their use
+      if (slot == (pv_first >= PFV ? pv_first - PFV : 0)) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const half2v pr = {pf[ks][2 * e], pf[ks][2 * e + 1]};
-        l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
+        for (int v = 0; v < PFV; ++v) vf[v] = read_v(Vc, v);
       }
-    }
-
-    // ---- O^T += V_j^T P_j^T -----------------------------------------------
-    // Key order of 16-key step ks (sub-tile t = ks/2, half s = ks%2):
-    // element e of the lane's 8 = key 32t + 16s + 8(e/4) + 4*hi + e%4.
-    const _Float16* Vs = smem + (2 + (j & 1)) * L::Tile;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int imm = 16 * ks * L::Pitch + 32 * mt;
-        const half4 lo = ds_read_tr16(Vs + v_base0 + imm);
-        const half4 hi4 = ds_read_tr16(Vs + v_base1 + imm);
-        const half8 vf = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-        oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], oacc[mt], 0, 0, 0);
+      if (slot >= pv_first) {
+        const int v = slot - pv_first + PFV;
+        if (v < NPV) vf[v] = read_v(Vc, v);
       }
+      // the MFMA of this slot
+      if (slot < pv_first) {
+        const int i = nsa + slot;
+        if (i + PFK < ns) kf[i + PFK] = read_k(Kn, i + PFK);
+        const int t = i / KK, kk = i % KK;
+        s_nxt[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            kf[i], qf[kk], kk == 0 ? (float16v)0.0f : s_nxt[t], 0, 0, 0);
+      } else {
+        const int v = slot - pv_first;
+        const int ks = v / MT, mt = v % MT;
+        oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[v], pf[ks], oacc[mt], 0, 0, 0);
+      }
+      // softmax pairs assigned to this slot
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        if (pair_slot(p) == slot) softmax_pair(p);
+      }
+      fence_schedule();
     }
 
     if (HAS_NEXT) {
-      if (more2) store_k(j & 1);
-      store_v((j + 1) & 1);
-      __syncthreads();
+      barrier_after_direct_loads();  // V_{j+1}, K_{j+2} landed; V_j, K_{j+1} reads done
 #pragma unroll
       for (int t = 0; t < 2; ++t) s_cur[t] = s_nxt[t];
     }
@@ -337,18 +408,20 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
 
   // ---- prologue: K_0, V_0, K_1 into LDS; S_0 -------------------------------
   if (ntiles > 0) {
-    load_k(0);
-    load_v(0);
-    store_k(0);
-    store_v(0);
-    if (ntiles > 1) {
-      load_k(1);
-      store_k(1);
-    }
+    load_k(0, 0);
+    load_v(0, 0);
+    if (ntiles > 1) load_k(1, 1);
   }
-  __syncthreads();
+  barrier_after_direct_loads();
   if (ntiles > 0) {
-    qk(smem, s_cur);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s_cur[t] = (float16v)0.0f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        s_cur[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(smem, t * KK + kk), qf[kk],
+                                                          s_cur[t], 0, 0, 0);
+    }
     for (int j = 0; j + 1 < ntiles; ++j) step(j, Flag<true>{});
     step(ntiles - 1, Flag<false>{});
   }
