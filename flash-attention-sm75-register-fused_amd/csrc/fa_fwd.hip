@@ -155,7 +155,14 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   constexpr int SEGW = L::SegsPerWave;
 
   // [K buffer 0 | K buffer 1 | V buffer 0 | V buffer 1]
-  __shared__ __attribute__((aligned(1024))) _Float16 smem[4 * L::Tile];
+  // Four distinct objects (not one array): the loop is unrolled by two, so
+  // every access names its buffer at compile time and the compiler can see
+  // that the in-flight direct loads never alias the tiles being read (it
+  // would otherwise drain vmcnt before each LDS read).
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds0[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds1[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds0[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds1[L::Tile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -220,22 +227,29 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const int k_all_bytes = (int)(N * a.ksn * 2);
   const int v_all_bytes = (int)(N * a.vsn * 2);
 
-  auto lds_seg = [&](int tile_index, int s) -> lds_void* {
-    return (lds_void*)(smem + tile_index * L::Tile + (wave + kWaves * s) * 512);
+  // Buffer selection by compile-time parity.
+  auto kbuf = [&](auto par) -> _Float16* {
+    if constexpr (decltype(par)::value) return k_lds1; else return k_lds0;
   };
-  auto load_k = [&](int j, int buf) {
+  auto vbuf = [&](auto par) -> _Float16* {
+    if constexpr (decltype(par)::value) return v_lds1; else return v_lds0;
+  };
+  auto lds_seg = [&](_Float16* tile, int s) -> lds_void* {
+    return (lds_void*)(tile + (wave + kWaves * s) * 512);
+  };
+  auto load_k = [&](int j, _Float16* dst) {
     const __amdgpu_buffer_rsrc_t r =
         make_rsrc(Kp + (int64_t)j * kBlockN * a.ksn, k_all_bytes - j * k_tile_bytes);
 #pragma unroll
     for (int s = 0; s < SEGW; ++s)
-      direct_load16(r, lds_seg(buf, s), goff_k[s]);
+      direct_load16(r, lds_seg(dst, s), goff_k[s]);
   };
-  auto load_v = [&](int j, int buf) {
+  auto load_v = [&](int j, _Float16* dst) {
     const __amdgpu_buffer_rsrc_t r =
         make_rsrc(Vp + (int64_t)j * kBlockN * a.vsn, v_all_bytes - j * v_tile_bytes);
 #pragma unroll
     for (int s = 0; s < SEGW; ++s)
-      direct_load16(r, lds_seg(2 + buf, s), goff_v[s]);
+      direct_load16(r, lds_seg(dst, s), goff_v[s]);
   };
 
   // Per-lane LDS bases of the operand reads (see Lds): K rows ql (+32t),
@@ -273,18 +287,20 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
 
   float16v s_cur[2], s_nxt[2];
 
-  // One pipeline step for tile j.  HAS_NEXT: tile j+1 exists, so S_{j+1} is
-  // computed here and the loads of V_{j+1} (and K_{j+2}) are issued.
-  auto step = [&](int j, auto has_next_t) {
+  // One pipeline step for tile j (PAR = j & 1).  HAS_NEXT: tile j+1 exists,
+  // so S_{j+1} is computed here and the loads of V_{j+1} (and K_{j+2}) are
+  // issued.
+  auto step = [&](int j, auto has_next_t, auto par_t) {
     constexpr bool HAS_NEXT = decltype(has_next_t)::value;
+    constexpr bool PAR = decltype(par_t)::value;
     constexpr int ns = HAS_NEXT ? NS : 0;     // S MFMAs this step
     constexpr int nsa = HAS_NEXT ? NSA : 0;   // ... of which in the max block
-    const _Float16* Kn = smem + ((j + 1) & 1) * L::Tile;
-    const _Float16* Vc = smem + (2 + (j & 1)) * L::Tile;
+    const _Float16* Kn = kbuf(Flag<!PAR>{});
+    const _Float16* Vc = vbuf(Flag<PAR>{});
 
     if (HAS_NEXT) {
-      if (j + 2 < ntiles) load_k(j + 2, j & 1);
-      load_v(j + 1, (j + 1) & 1);
+      if (j + 2 < ntiles) load_k(j + 2, kbuf(Flag<PAR>{}));
+      load_v(j + 1, vbuf(Flag<!PAR>{}));
     }
 
     // ---- mask (sequence tail, causal diagonal) --------------------------
@@ -408,9 +424,9 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
 
   // ---- prologue: K_0, V_0, K_1 into LDS; S_0 -------------------------------
   if (ntiles > 0) {
-    load_k(0, 0);
-    load_v(0, 0);
-    if (ntiles > 1) load_k(1, 1);
+    load_k(0, k_lds0);
+    load_v(0, v_lds0);
+    if (ntiles > 1) load_k(1, k_lds1);
   }
   barrier_after_direct_loads();
   if (ntiles > 0) {
@@ -419,11 +435,20 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
       s_cur[t] = (float16v)0.0f;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
-        s_cur[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(smem, t * KK + kk), qf[kk],
+        s_cur[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(k_lds0, t * KK + kk), qf[kk],
                                                           s_cur[t], 0, 0, 0);
     }
-    for (int j = 0; j + 1 < ntiles; ++j) step(j, Flag<true>{});
-    step(ntiles - 1, Flag<false>{});
+    int j = 0;
+    for (; j + 2 < ntiles; j += 2) {
+      step(j, Flag<true>{}, Flag<false>{});
+      step(j + 1, Flag<true>{}, Flag<true>{});
+    }
+    if (j + 1 < ntiles) {
+      step(j, Flag<true>{}, Flag<false>{});
+      step(j + 1, Flag<false>{}, Flag<true>{});
+    } else {
+      step(j, Flag<false>{}, Flag<false>{});
+    }
   }
 
   // ---- epilogue: combine the two half-wave partial sums, normalise, store ---
