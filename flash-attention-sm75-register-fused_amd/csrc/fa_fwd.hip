@@ -140,9 +140,10 @@ struct Flag {
 // Software-pipelined main loop: iteration j computes S^T_{j+1} = K_{j+1} Q^T
 // while the VALU turns S^T_j into probabilities, then accumulates P_j V_j.
 // LDS holds two K and two V tiles; the direct loads of K_{j+2} and V_{j+1}
-// issued at the top of iteration j land in the buffers iteration j-1 freed,
-// so one barrier per iteration suffices.
-template <int D, bool CAUSAL>
+// issued during iteration j land in the buffers iteration j-1 freed, so one
+// barrier per iteration suffices.  KV_SAME_STRIDE: K and V rows have the
+// same stride, so V's direct-load offsets are K's (saves registers).
+template <int D, bool CAUSAL, bool KV_SAME_STRIDE>
 __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   using L = Lds<D>;
   constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
@@ -207,7 +208,8 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   // Direct-load map: wave w fills 1 KB segments w, w + 4, ...; lane l of a
   // segment covers tile bytes [1024 seg + 16 l, +16).  Precompute the global
   // byte offset inside a tile for each segment (padding lanes: past the end).
-  int goff_k[SEGW], goff_v[SEGW];
+  int goff_k[SEGW], goff_v_own[KV_SAME_STRIDE ? 1 : SEGW];
+  int* goff_v = KV_SAME_STRIDE ? goff_k : goff_v_own;
 #pragma unroll
   for (int s = 0; s < SEGW; ++s) {
     const int pos = (wave + kWaves * s) * 1024 + 16 * lane;  // bytes into the tile
@@ -216,10 +218,10 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
     if (within < 2 * D) {
       const int c = (within >> 4) ^ ((row >> 2) & 3);
       goff_k[s] = (int)(row * a.ksn * 2) + 16 * c;
-      goff_v[s] = (int)(row * a.vsn * 2) + 16 * c;
+      if (!KV_SAME_STRIDE) goff_v[s] = (int)(row * a.vsn * 2) + 16 * c;
     } else {
       goff_k[s] = -16;  // 0xfffffff0: beyond any window -> writes zeros
-      goff_v[s] = -16;
+      if (!KV_SAME_STRIDE) goff_v[s] = -16;
     }
   }
   const int k_tile_bytes = (int)(kBlockN * a.ksn * 2);
@@ -236,6 +238,15 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   };
   auto lds_seg = [&](_Float16* tile, int s) -> lds_void* {
     return (lds_void*)(tile + (wave + kWaves * s) * 512);
+  };
+  // Buffer windows of tile j (empty past the last tile: every lane reads 0).
+  auto k_window = [&](int j) {
+    const int bytes = k_all_bytes - j * k_tile_bytes;
+    return make_rsrc(Kp + (int64_t)j * kBlockN * a.ksn, bytes > 0 ? bytes : 0);
+  };
+  auto v_window = [&](int j) {
+    const int bytes = v_all_bytes - j * v_tile_bytes;
+    return make_rsrc(Vp + (int64_t)j * kBlockN * a.vsn, bytes > 0 ? bytes : 0);
   };
   auto load_k = [&](int j, _Float16* dst) {
     const __amdgpu_buffer_rsrc_t r =
@@ -298,10 +309,22 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
     const _Float16* Kn = kbuf(Flag<!PAR>{});
     const _Float16* Vc = vbuf(Flag<PAR>{});
 
+    // Direct loads of K_{j+2} (empty window past the end) and V_{j+1}; one
+    // 1 KB segment is issued after each of the first MFMAs of block B, so
+    // the address unit's queueing overlaps MFMA execution.
+    __amdgpu_buffer_rsrc_t rk_next, rv_next;
     if (HAS_NEXT) {
-      if (j + 2 < ntiles) load_k(j + 2, kbuf(Flag<PAR>{}));
-      load_v(j + 1, vbuf(Flag<!PAR>{}));
+      rk_next = k_window(j + 2);
+      rv_next = v_window(j + 1);
     }
+    _Float16* k_dst = kbuf(Flag<PAR>{});
+    _Float16* v_dst = vbuf(Flag<!PAR>{});
+    auto issue_load = [&](int q) {  // q < SEGW: K segment q, else V segment q - SEGW
+      if (q < SEGW)
+        direct_load16(rk_next, lds_seg(k_dst, q), goff_k[q]);
+      else
+        direct_load16(rv_next, lds_seg(v_dst, q - SEGW), goff_v[q - SEGW]);
+    };
 
     // ---- mask (sequence tail, causal diagonal) --------------------------
     const int kstart = j * kBlockN;
@@ -407,6 +430,13 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
         const int ks = v / MT, mt = v % MT;
         oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[v], pf[ks], oacc[mt], 0, 0, 0);
       }
+      // direct loads spread over the first half of block B
+      if (HAS_NEXT) {
+#pragma unroll
+        for (int q = 0; q < 2 * SEGW; ++q) {
+          if ((q * (NB / 2)) / (2 * SEGW) == slot) issue_load(q);
+        }
+      }
       // softmax pairs assigned to this slot
 #pragma unroll
       for (int p = 0; p < 16; ++p) {
@@ -483,17 +513,23 @@ int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
   args.num_qblocks = (int)nblocks;
   const dim3 grid((unsigned)(batch * a.hq), (unsigned)nblocks);
   const dim3 block(kThreads);
+  const bool same = a.ksn == a.vsn;
+#define FA_LAUNCH(D, C, S) \
+  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S>), grid, block, 0, stream, args)
   if (head_dim == 128) {
-    if (causal)
-      hipLaunchKernelGGL((fa_fwd_kernel<128, true>), grid, block, 0, stream, args);
-    else
-      hipLaunchKernelGGL((fa_fwd_kernel<128, false>), grid, block, 0, stream, args);
+    if (causal) {
+      if (same) FA_LAUNCH(128, true, true); else FA_LAUNCH(128, true, false);
+    } else {
+      if (same) FA_LAUNCH(128, false, true); else FA_LAUNCH(128, false, false);
+    }
   } else {
-    if (causal)
-      hipLaunchKernelGGL((fa_fwd_kernel<64, true>), grid, block, 0, stream, args);
-    else
-      hipLaunchKernelGGL((fa_fwd_kernel<64, false>), grid, block, 0, stream, args);
+    if (causal) {
+      if (same) FA_LAUNCH(64, true, true); else FA_LAUNCH(64, true, false);
+    } else {
+      if (same) FA_LAUNCH(64, false, true); else FA_LAUNCH(64, false, false);
+    }
   }
+#undef FA_LAUNCH
   return 0;
 }
 
