@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
 #include <cstring>
 
 #include "fa_internal.h"
@@ -16,6 +17,9 @@
 namespace {
 
 thread_local char g_last_error[512] = "";
+
+// Which fused kernel fa_sm75_forward launches (process-wide).
+std::atomic<int> g_kernel_policy{FA_POLICY_AUTO};
 
 int fail(int status, const char* fmt, ...) {
   va_list ap;
@@ -167,9 +171,18 @@ int fa_sm75_forward(const fa_fwd_params* p) {
   if (p->batch == 0 || p->heads_q == 0 || p->seq_len == 0) return FA_OK;
   const fa::FwdArgs a = make_args(p);
   fa::launch_fused_forward(a, (int)p->batch, (int)p->head_dim, p->causal != 0,
+                           g_kernel_policy.load(std::memory_order_relaxed),
                            reinterpret_cast<hipStream_t>(p->stream));
   return check_launch();
 }
+
+int fa_sm75_set_kernel_policy(int policy) {
+  if (policy < FA_POLICY_AUTO || policy > FA_POLICY_WIDE) return FA_ERR_INVALID_ARGUMENT;
+  g_kernel_policy.store(policy, std::memory_order_relaxed);
+  return FA_OK;
+}
+
+int fa_sm75_get_kernel_policy(void) { return g_kernel_policy.load(std::memory_order_relaxed); }
 
 int fa_sm75_naive_forward(const fa_fwd_params* p, float* workspace) {
   g_last_error[0] = '\0';

@@ -46,96 +46,10 @@
 
 #include "fa_internal.h"
 
+#include "fa_kernel_common.h"
+
 namespace fa {
 namespace {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef short short4v __attribute__((ext_vector_type(4)));
-typedef float float16v __attribute__((ext_vector_type(16)));
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kBlockM = 32 * kWaves;  // queries per workgroup
-constexpr int kBlockN = 64;           // keys per LDS tile
-// Online-softmax rescale threshold (log2 units): the running max used for
-// the exponent is only raised when a row's tile max exceeds it by more than
-// this, so P stays <= 2^8 and the O/l rescale is skipped for most tiles.
-// The result is mathematically unchanged (l and O use the same stale max).
-constexpr float kRescaleLog2 = 8.0f;
-
-// LDS tile layout: row r of a K or V tile starts at r * Pitch halves, with
-// Pitch = D + 32 (64 bytes of padding per row), and its 16-byte chunk c is
-// stored at chunk position c ^ ((r >> 2) & 3).  The padding shifts each row
-// by 64 bytes modulo the 256-byte bank sweep, the XOR spreads the 4 rows of
-// each aligned group over the 4 chunks of a 64-byte block.  Together:
-//  * K operand reads (ds_read_b128, 16 lanes = 16 consecutive rows, one
-//    chunk) hit 16 distinct 16-byte bank groups;
-//  * transposing V reads (ds_read_b64_tr_b16, 32 lanes = 4 rows x two
-//    32-byte chunk pairs) hit 8 distinct pair slots;
-//  * the XOR only touches the low two chunk bits, so every address is a
-//    per-lane base plus a compile-time immediate.
-// A tile is written by whole-wave direct loads of 1 KB segments; lanes whose
-// 16 bytes fall in the padding load from past the buffer window (zeros).
-template <int D>
-struct Lds {
-  static constexpr int Pitch = D + 32;           // halves per row
-  static constexpr int Tile = kBlockN * Pitch;   // halves per K (or V) tile
-  static constexpr int Segs = Tile * 2 / 1024;   // 1 KB direct-load segments
-  static constexpr int SegsPerWave = Segs / kWaves;
-  static_assert(Segs % kWaves == 0, "segments must split over the waves");
-};
-
-__device__ __forceinline__ half4 ds_read_tr16(const _Float16* p) {
-  short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) short4v*)(p));
-  return __builtin_bit_cast(half4, r);
-}
-
-// Combines the two half-wave copies of a per-query value (lanes l and l^32):
-// v_permlane32_swap(x, x) yields [x_lo, x_lo] and [x_hi, x_hi].
-__device__ __forceinline__ float halves_max(float x) {
-  const unsigned u = __builtin_bit_cast(unsigned, x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
-}
-__device__ __forceinline__ float halves_sum(float x) {
-  const unsigned u = __builtin_bit_cast(unsigned, x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
-}
-
-// Raw buffer resource over [base, base + bytes): loads past the end return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes,
-                                           0x00020000);
-}
-
-// 16 bytes per lane from a buffer window straight into LDS (lane l writes
-// dst + 16 l).  Kept out of line of the kernel template so the host pass
-// still emits the kernel's launch stub.
-__device__ __forceinline__ void direct_load16(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
-}
-
-// Freezes the instruction order at this point (nothing is moved across).
-__device__ __forceinline__ void fence_schedule() { __builtin_amdgcn_sched_barrier(0); }
-
-// Workgroup barrier that also publishes this wave's direct-to-LDS loads:
-// they are counted by vmcnt, which the compiler does not drain before
-// s_barrier on its own.  0x0F70 = vmcnt(0) expcnt(7) lgkmcnt(15) (gfx9).
-__device__ __forceinline__ void barrier_after_direct_loads() {
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  __syncthreads();
-}
-
-template <bool B>
-struct Flag {
-  static constexpr bool value = B;
-};
 
 // Software-pipelined main loop: iteration j computes S^T_{j+1} = K_{j+1} Q^T
 // while the VALU turns S^T_j into probabilities, then accumulates P_j V_j.
@@ -150,7 +64,6 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   constexpr int MT = D / 32;       // 32-row output tiles of O^T
   constexpr int NS = 2 * KK;       // S^T MFMAs per tile
   constexpr int NPV = 4 * MT;      // P V MFMAs per tile
-  constexpr int NSA = 4;           // S^T MFMAs issued while the row max is formed
   constexpr int PFK = 3;           // K operand reads run this many MFMAs ahead
   constexpr int PFV = 2;           // V operand reads run this many MFMAs ahead
   constexpr int SEGW = L::SegsPerWave;
@@ -296,22 +209,68 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const float c2 = a.c;  // |scale| * log2(e)
   const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-  float16v s_cur[2], s_nxt[2];
+  // S^T of two tiles in flight, ping-pong by tile parity (no copies): the
+  // step for tile j reads s_buf[j & 1] and fills s_buf[(j + 1) & 1].
+  float16v s_buf[2][2];
+  auto row_max = [](const float16v (&s)[2]) {
+    float m0 = s[0][0], m1 = s[1][0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+      m0 = fmaxf(m0, s[0][i]);
+      m1 = fmaxf(m1, s[1][i]);
+    }
+    return fmaxf(m0, m1);
+  };
+  float mc = 0.0f;  // running max of tile j's rows, times c2 (exp2 offset)
 
-  // One pipeline step for tile j (PAR = j & 1).  HAS_NEXT: tile j+1 exists,
-  // so S_{j+1} is computed here and the loads of V_{j+1} (and K_{j+2}) are
-  // issued.
+  // Prepares tile j's scores for its softmax: masks them if tile j crosses
+  // the sequence end or this wave's causal diagonal (the unmasked row max mx
+  // is then recomputed), raises the running max when some row outgrew it by
+  // more than 2^kRescaleLog2 (rescaling O and l), and sets mc.
+  auto prepare = [&](int j, float16v (&s)[2], float mx) {
+    const int kstart = j * kBlockN;
+    const bool need_mask = (kstart + kBlockN > N) || (CAUSAL && kstart + kBlockN - 1 > qw);
+    if (need_mask) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
+          const bool masked = (key >= N) || (CAUSAL && key > qrow);
+          if (masked) s[t][i] = -__builtin_inff();
+        }
+      }
+      mx = halves_max(row_max(s));
+    }
+    const bool grow = (mx - m_run) * c2 > kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
+      const float alpha =
+          (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) oacc[mt] *= alpha;
+      m_run = m_new;
+    }
+    mc = ((m_run == -__builtin_inff()) ? 0.0f : m_run) * c2;
+  };
+
+  // One pipeline step for tile j (PAR = j & 1), whose scores are prepared.
+  // HAS_NEXT: tile j+1 exists, so S_{j+1} is computed (and prepared) here
+  // and the loads of V_{j+1} (and K_{j+2}) are issued.
   auto step = [&](int j, auto has_next_t, auto par_t) {
     constexpr bool HAS_NEXT = decltype(has_next_t)::value;
     constexpr bool PAR = decltype(par_t)::value;
     constexpr int ns = HAS_NEXT ? NS : 0;     // S MFMAs this step
-    constexpr int nsa = HAS_NEXT ? NSA : 0;   // ... of which in the max block
     const _Float16* Kn = kbuf(Flag<!PAR>{});
     const _Float16* Vc = vbuf(Flag<PAR>{});
+    float16v (&s_cur)[2] = s_buf[PAR ? 1 : 0];
+    float16v (&s_nxt)[2] = s_buf[PAR ? 0 : 1];
 
-    // Direct loads of K_{j+2} (empty window past the end) and V_{j+1}; one
-    // 1 KB segment is issued after each of the first MFMAs of block B, so
-    // the address unit's queueing overlaps MFMA execution.
+    // Direct loads of K_{j+2} (empty window past the end) and V_{j+1}, one
+    // 1 KB segment after each of the first MFMAs, so the address unit's
+    // queueing overlaps MFMA execution.
     __amdgpu_buffer_rsrc_t rk_next, rv_next;
     if (HAS_NEXT) {
       rk_next = k_window(j + 2);
@@ -326,75 +285,36 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
         direct_load16(rv_next, lds_seg(v_dst, q - SEGW), goff_v[q - SEGW]);
     };
 
-    // ---- mask (sequence tail, causal diagonal) --------------------------
-    const int kstart = j * kBlockN;
-    const bool need_mask = (kstart + kBlockN > N) || (CAUSAL && kstart + kBlockN - 1 > qw);
-    if (need_mask) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
-          const bool masked = (key >= N) || (CAUSAL && key > qrow);
-          if (masked) s_cur[t][i] = -__builtin_inff();
-        }
-      }
-    }
-
-    // ---- block A: first S_{j+1} MFMAs while the row max is formed --------
-    half8 kf[NS > 0 ? NS : 1];
-#pragma unroll
-    for (int i = 0; i < PFK && i < ns; ++i) kf[i] = read_k(Kn, i);
-    float mx = -__builtin_inff();
-    constexpr int MAXA = nsa > 0 ? nsa : 1;   // slots the max is spread over
-#pragma unroll
-    for (int slot = 0; slot < MAXA; ++slot) {
-      if (slot < nsa) {
-        const int i = slot;
-        if (i + PFK < ns) kf[i + PFK] = read_k(Kn, i + PFK);
-        const int t = i / KK, kk = i % KK;
-        s_nxt[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            kf[i], qf[kk], kk == 0 ? (float16v)0.0f : s_nxt[t], 0, 0, 0);
-      }
-#pragma unroll
-      for (int e = slot * 32 / MAXA; e < (slot + 1) * 32 / MAXA; ++e)
-        mx = fmaxf(mx, s_cur[e >> 4][e & 15]);
-      fence_schedule();
-    }
-    mx = halves_max(mx);
-
-    // ---- raise the running max only when some row outgrew it by 2^8 -----
-    const bool grow = (mx - m_run) * c2 > kRescaleLog2;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
-      const float alpha =
-          (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * c2);
-      l_run *= alpha;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) oacc[mt] *= alpha;
-      m_run = m_new;
-    }
-    const float mc = ((m_run == -__builtin_inff()) ? 0.0f : m_run) * c2;
-
-    // ---- block B: remaining S_{j+1} MFMAs, then P_j V_j; the softmax of --
-    // S_j (16 pairs of scores) is spread over the slots.  Within a slot the
-    // MFMA is issued first, so the pairs of 16-key step ks must sit in a
-    // slot before the first P V MFMA of step ks; pairs that cannot (the
-    // last tile has no S MFMAs to hide them behind) go before the loop.
-    constexpr int NB = (ns - nsa) + NPV;            // MFMA slots in block B
-    constexpr int PV_FIRST = ns - nsa;              // slot of the first P V MFMA
+    // ---- slots: S_{j+1} MFMAs, then P_j V_j --------------------------------
+    // The softmax of S_j (16 pairs of scores) is spread over the slots.
+    // Within a slot the MFMA is issued first, so the pairs of 16-key step ks
+    // must sit in a slot before the first P V MFMA of step ks; pairs that
+    // cannot (the last tile has no S MFMAs to hide them behind) go first.
+    constexpr int NB = ns + NPV;                    // MFMA slots
+    constexpr int PV_FIRST = ns;                    // slot of the first P V MFMA
     constexpr int PAIR_SLOTS = NB - MT;             // slots available to pairs
+    half8 kf[NS];
     half8 pf[4];
     half8 vf[NPV];
-    auto pair_slot = [&](int p) {
+    constexpr auto pair_slot = [](int p) constexpr {
       const int spread = (p * PAIR_SLOTS) / 16;
       const int last_ok = PV_FIRST + (p / 4) * MT - 1;
       return spread < last_ok ? spread : last_ok;
     };
-    auto softmax_pair = [&](int p) {
-      const int e = 2 * p;
+    // Row max of S_{j+1}: element e (sub-tile t = e / 16) is folded in at
+    // max_slot(e), a few slots after the last MFMA into sub-tile t; the lane
+    // swap of the two wave halves sits in the last slot.
+    constexpr auto max_slot = [](int e) constexpr {
       const int t = e >> 4, i = e & 15;
+      const int first = (t + 1) * KK + 2;
+      const int span = (t == 0 ? KK : NB - 1 - first);
+      const int s = first + (i * span) / 16;
+      return s < NB - 1 ? s : NB - 1;
+    };
+    auto softmax_pair = [&](auto p_c) {
+      constexpr int p = decltype(p_c)::value;
+      constexpr int e = 2 * p;
+      constexpr int t = e >> 4, i = e & 15;
       const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i], c2, -mc));
       const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i + 1], c2, -mc));
       const half2v pr = {(_Float16)p0, (_Float16)p1};
@@ -402,53 +322,54 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
       pf[2 * t + (i >> 3)][(i & 7) + 1] = pr[1];
       l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
     };
-#pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      if (pair_slot(p) < 0) softmax_pair(p);
-    }
-#pragma unroll
-    for (int slot = 0; slot < NB; ++slot) {
-      const int pv_first = PV_FIRST;
+    static_for<16>([&](auto p_c) {
+      if constexpr (pair_slot(decltype(p_c)::value) < 0) softmax_pair(p_c);
+    });
+    static_for<(PFK < ns ? PFK : ns)>([&](auto i_c) {
+      kf[decltype(i_c)::value] = read_k(Kn, decltype(i_c)::value);
+    });
+    float mx_next = -__builtin_inff();
+    static_for<NB>([&](auto slot_c) {
+      constexpr int slot = decltype(slot_c)::value;
       // V operand reads, PFV MFMAs ahead of their use
-      if (slot == (pv_first >= PFV ? pv_first - PFV : 0)) {
-#pragma unroll
-        for (int v = 0; v < PFV; ++v) vf[v] = read_v(Vc, v);
+      if constexpr (slot == (PV_FIRST >= PFV ? PV_FIRST - PFV : 0)) {
+        static_for<PFV>([&](auto v_c) { vf[decltype(v_c)::value] = read_v(Vc, decltype(v_c)::value); });
       }
-      if (slot >= pv_first) {
-        const int v = slot - pv_first + PFV;
-        if (v < NPV) vf[v] = read_v(Vc, v);
+      if constexpr (slot >= PV_FIRST && slot - PV_FIRST + PFV < NPV) {
+        vf[slot - PV_FIRST + PFV] = read_v(Vc, slot - PV_FIRST + PFV);
       }
       // the MFMA of this slot
-      if (slot < pv_first) {
-        const int i = nsa + slot;
-        if (i + PFK < ns) kf[i + PFK] = read_k(Kn, i + PFK);
-        const int t = i / KK, kk = i % KK;
+      if constexpr (slot < PV_FIRST) {
+        constexpr int i = slot;
+        if constexpr (i + PFK < ns) kf[i + PFK] = read_k(Kn, i + PFK);
+        constexpr int t = i / KK, kk = i % KK;
         s_nxt[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
             kf[i], qf[kk], kk == 0 ? (float16v)0.0f : s_nxt[t], 0, 0, 0);
       } else {
-        const int v = slot - pv_first;
-        const int ks = v / MT, mt = v % MT;
+        constexpr int v = slot - PV_FIRST;
+        constexpr int ks = v / MT, mt = v % MT;
         oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[v], pf[ks], oacc[mt], 0, 0, 0);
       }
-      // direct loads spread over the first half of block B
-      if (HAS_NEXT) {
-#pragma unroll
-        for (int q = 0; q < 2 * SEGW; ++q) {
-          if ((q * (NB / 2)) / (2 * SEGW) == slot) issue_load(q);
-        }
+      if constexpr (HAS_NEXT) {
+        static_for<2 * SEGW>([&](auto q_c) {
+          constexpr int q = decltype(q_c)::value;
+          if constexpr ((q * (NB / 2)) / (2 * SEGW) == slot) issue_load(q);
+        });
+        static_for<32>([&](auto e_c) {
+          constexpr int e = decltype(e_c)::value;
+          if constexpr (max_slot(e) == slot) mx_next = fmaxf(mx_next, s_nxt[e >> 4][e & 15]);
+        });
+        if constexpr (slot == NB - 1) mx_next = halves_max(mx_next);
       }
-      // softmax pairs assigned to this slot
-#pragma unroll
-      for (int p = 0; p < 16; ++p) {
-        if (pair_slot(p) == slot) softmax_pair(p);
-      }
+      static_for<16>([&](auto p_c) {
+        if constexpr (pair_slot(decltype(p_c)::value) == slot) softmax_pair(p_c);
+      });
       fence_schedule();
-    }
+    });
 
     if (HAS_NEXT) {
+      prepare(j + 1, s_nxt, mx_next);
       barrier_after_direct_loads();  // V_{j+1}, K_{j+2} landed; V_j, K_{j+1} reads done
-#pragma unroll
-      for (int t = 0; t < 2; ++t) s_cur[t] = s_nxt[t];
     }
   };
 
@@ -462,12 +383,13 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   if (ntiles > 0) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      s_cur[t] = (float16v)0.0f;
+      s_buf[0][t] = (float16v)0.0f;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
-        s_cur[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(k_lds0, t * KK + kk), qf[kk],
-                                                          s_cur[t], 0, 0, 0);
+        s_buf[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(k_lds0, t * KK + kk), qf[kk],
+                                                             s_buf[0][t], 0, 0, 0);
     }
+    prepare(0, s_buf[0], halves_max(row_max(s_buf[0])));
     int j = 0;
     for (; j + 2 < ntiles; j += 2) {
       step(j, Flag<true>{}, Flag<false>{});
@@ -506,14 +428,27 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
 
 }  // namespace
 
+// Whether the automatic policy may pick the 256-row kernel.  Off: it needs
+// more than the 512 registers per lane a wave can hold and spills, so it is
+// only reachable through FA_POLICY_WIDE.
+constexpr bool kAutoWide = false;
+
 int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
-                         hipStream_t stream) {
+                         int policy, hipStream_t stream) {
+  const bool same = a.ksn == a.vsn;
+  const dim3 block(kThreads);
+  // The wide kernel (256 rows per workgroup, one workgroup per CU) when there
+  // are enough workgroups to give every CU at least two.  It assumes a
+  // non-negative scale (the narrow kernel negates Q for the other case).
+  const int64_t wide_blocks = ((int64_t)a.n + kBlockMWide - 1) / kBlockMWide;
+  const bool wide = head_dim == 128 && !a.negate_q &&
+                    (policy == 2 || (policy == 0 && kAutoWide &&
+                                     (int64_t)batch * a.hq * wide_blocks >= 512));
+  if (wide) return launch_fused_forward_wide(a, batch, causal, stream);
   const int64_t nblocks = ((int64_t)a.n + kBlockM - 1) / kBlockM;
   FwdArgs args = a;
   args.num_qblocks = (int)nblocks;
   const dim3 grid((unsigned)(batch * a.hq), (unsigned)nblocks);
-  const dim3 block(kThreads);
-  const bool same = a.ksn == a.vsn;
 #define FA_LAUNCH(D, C, S) \
   hipLaunchKernelGGL((fa_fwd_kernel<D, C, S>), grid, block, 0, stream, args)
   if (head_dim == 128) {

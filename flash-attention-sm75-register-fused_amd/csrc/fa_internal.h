@@ -26,8 +26,14 @@ struct FwdArgs {
 };
 
 // Launches the fused MFMA kernel; all arguments already validated.
+// policy: 0 = choose by problem size, 1 = 128-row workgroups (two waves per
+// SIMD), 2 = 256-row workgroups (one wave per SIMD, head_dim 128 only).
 int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
-                         hipStream_t stream);
+                         int policy, hipStream_t stream);
+
+// 256-row workgroups (head_dim 128, scale >= 0); called by the above.
+constexpr int kBlockMWide = 256;
+int launch_fused_forward_wide(const FwdArgs& a, int batch, bool causal, hipStream_t stream);
 int fused_block_m();
 
 // Three-kernel path through an fp32 [B*Hq, N, N] score workspace.

@@ -1,0 +1,116 @@
+// Device-side building blocks shared by the fused attention kernels
+// (fa_fwd.hip: 128-row workgroups; fa_fwd_wide.hip: 256-row workgroups).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+#include <utility>
+
+namespace fa {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBlockM = 32 * kWaves;  // queries per workgroup
+constexpr int kBlockN = 64;           // keys per LDS tile
+// Online-softmax rescale threshold (log2 units): the running max used for
+// the exponent is only raised when a row's tile max exceeds it by more than
+// this, so P stays <= 2^8 and the O/l rescale is skipped for most tiles.
+// The result is mathematically unchanged (l and O use the same stale max).
+constexpr float kRescaleLog2 = 8.0f;
+
+// LDS tile layout: row r of a K or V tile starts at r * Pitch halves, with
+// Pitch = D + 32 (64 bytes of padding per row), and its 16-byte chunk c is
+// stored at chunk position c ^ ((r >> 2) & 3).  The padding shifts each row
+// by 64 bytes modulo the 256-byte bank sweep, the XOR spreads the 4 rows of
+// each aligned group over the 4 chunks of a 64-byte block.  Together:
+//  * K operand reads (ds_read_b128, 16 lanes = 16 consecutive rows, one
+//    chunk) hit 16 distinct 16-byte bank groups;
+//  * transposing V reads (ds_read_b64_tr_b16, 32 lanes = 4 rows x two
+//    32-byte chunk pairs) hit 8 distinct pair slots;
+//  * the XOR only touches the low two chunk bits, so every address is a
+//    per-lane base plus a compile-time immediate.
+// A tile is written by whole-wave direct loads of 1 KB segments; lanes whose
+// 16 bytes fall in the padding load from past the buffer window (zeros).
+template <int D>
+struct Lds {
+  static constexpr int Pitch = D + 32;           // halves per row
+  static constexpr int Tile = kBlockN * Pitch;   // halves per K (or V) tile
+  static constexpr int Segs = Tile * 2 / 1024;   // 1 KB direct-load segments
+  static constexpr int SegsPerWave = Segs / kWaves;
+  static_assert(Segs % kWaves == 0, "segments must split over the waves");
+};
+
+__device__ __forceinline__ half4 ds_read_tr16(const _Float16* p) {
+  short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4v*)(p));
+  return __builtin_bit_cast(half4, r);
+}
+
+// Combines the two half-wave copies of a per-query value (lanes l and l^32):
+// v_permlane32_swap(x, x) yields [x_lo, x_lo] and [x_hi, x_hi].
+__device__ __forceinline__ float halves_max(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+
+// Raw buffer resource over [base, base + bytes): loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes,
+                                           0x00020000);
+}
+
+// 16 bytes per lane from a buffer window straight into LDS (lane l writes
+// dst + 16 l).  Kept out of line of the kernel template so the host pass
+// still emits the kernel's launch stub.
+__device__ __forceinline__ void direct_load16(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
+}
+
+// Freezes the instruction order at this point (nothing is moved across).
+__device__ __forceinline__ void fence_schedule() { __builtin_amdgcn_sched_barrier(0); }
+
+// Workgroup barrier that also publishes this wave's direct-to-LDS loads:
+// they are counted by vmcnt, which the compiler does not drain before
+// s_barrier on its own.  0x0F70 = vmcnt(0) expcnt(7) lgkmcnt(15) (gfx9).
+__device__ __forceinline__ void barrier_after_direct_loads() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+}
+
+template <bool B>
+struct Flag {
+  static constexpr bool value = B;
+};
+
+// Compile-time loop: f(std::integral_constant<int, I>{}) for I = 0..N-1.
+// Used for the long slot schedules, which must expand completely (a rolled
+// loop would force the register arrays it indexes into scratch memory) and
+// are too large for the loop unroller's pragma threshold.
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+}  // namespace
+}  // namespace fa

@@ -92,6 +92,15 @@ const char* fa_sm75_status_string(int status);
 
 /* ABI version of this header (bumped on incompatible changes). */
 int fa_sm75_abi_version(void);
+
+/* Fused-kernel selection, process-wide (no reference counterpart: a tuning
+ * and testing control).  AUTO picks by problem size; NARROW forces 128-row
+ * workgroups (two waves per SIMD); WIDE forces 256-row workgroups (one wave
+ * per SIMD, 64 rows per wave; head_dim 128 only, head_dim 64 stays NARROW).
+ * Both kernels compute the same function. */
+enum fa_kernel_policy { FA_POLICY_AUTO = 0, FA_POLICY_NARROW = 1, FA_POLICY_WIDE = 2 };
+int fa_sm75_set_kernel_policy(int policy); /* FA_OK or FA_ERR_INVALID_ARGUMENT */
+int fa_sm75_get_kernel_policy(void);
 #define FA_SM75_ABI_VERSION 1
 
 /* ---- Reference launcher signatures ------------------------------------ */

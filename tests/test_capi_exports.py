@@ -112,3 +112,16 @@ def test_naive_validation(lib):
 
 def test_abi_version(lib):
     assert lib.fa_sm75_abi_version() == 1
+
+
+def test_kernel_policy_switch(lib):
+    lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
+    assert lib.fa_sm75_get_kernel_policy() == 0
+    assert lib.fa_sm75_set_kernel_policy(3) == 1
+    assert lib.fa_sm75_set_kernel_policy(-1) == 1
+    try:
+        for p in (1, 2, 0):
+            assert lib.fa_sm75_set_kernel_policy(p) == 0
+            assert lib.fa_sm75_get_kernel_policy() == p
+    finally:
+        lib.fa_sm75_set_kernel_policy(0)

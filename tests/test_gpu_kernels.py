@@ -1,0 +1,103 @@
+"""Both fused kernels against the oracle on the same inputs (needs a GPU).
+
+fa_sm75_forward picks between a 128-row workgroup kernel (two waves per
+SIMD) and a 256-row one (one wave per SIMD, 64 rows per wave, head_dim 128)
+by problem size; fa_sm75_set_kernel_policy forces either, so each is checked
+on the shapes the other would normally take.  Tolerance as in
+test_gpu_parity: |O - O_ref| <= 2e-3 + 1e-2 |O_ref|.
+"""
+import contextlib
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from capi_types import LIB
+from flash_attention_sm75 import flash_attention_forward, flash_attention_forward_lse
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+NARROW, WIDE = 1, 2
+
+
+@contextlib.contextmanager
+def policy(p):
+    lib = ctypes.CDLL(LIB)
+    lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
+    assert lib.fa_sm75_set_kernel_policy(p) == 0
+    try:
+        yield
+    finally:
+        lib.fa_sm75_set_kernel_policy(0)
+
+
+def inputs(B, Hq, Hkv, N, D, seed, std=1.0):
+    g = torch.Generator("cpu").manual_seed(seed)
+    q = (torch.randn(B, Hq, N, D, generator=g) * std).half()
+    k = (torch.randn(B, Hkv, N, D, generator=g) * std).half()
+    v = (torch.randn(B, Hkv, N, D, generator=g) * std).half()
+    return q, k, v
+
+
+def check(out, q, k, v, causal, scale=None, label=""):
+    expect = ref.attention_reference_chunked(q.numpy(), k.numpy(), v.numpy(), causal=causal,
+                                             scale=scale, return_f32=True)
+    res = ref.check_correctness(out.float().cpu().numpy(), expect, atol=2e-3, rtol=1e-2)
+    print(f"  {label}: max_abs={res['max_abs_err']:.3e}", flush=True)
+    assert res["allclose"], res
+
+
+SHAPES = [
+    # B, Hq, Hkv, N, D, causal
+    (1, 2, 2, 1, 128, False),
+    (1, 2, 2, 63, 128, True),
+    (1, 2, 1, 200, 128, True),
+    (1, 4, 2, 256, 128, False),
+    (1, 4, 1, 257, 128, True),
+    (2, 8, 2, 511, 128, True),
+    (1, 4, 4, 700, 128, False),
+    (1, 3, 1, 1030, 128, True),
+    (1, 2, 2, 300, 64, True),
+]
+
+
+@pytest.mark.parametrize("pol", [NARROW, WIDE], ids=["narrow", "wide"])
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal", SHAPES)
+def test_forced_policy(device, pol, B, Hq, Hkv, N, D, causal):
+    print(f"[policy {pol}] B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal}", flush=True)
+    q, k, v = inputs(B, Hq, Hkv, N, D, seed=N + 7 * Hq)
+    with policy(pol):
+        out = flash_attention_forward(q.to(device), k.to(device), v.to(device), causal=causal)
+        torch.cuda.synchronize()
+    check(out, q, k, v, causal, label=f"pol{pol} N{N} D{D}")
+
+
+@pytest.mark.parametrize("pol", [NARROW, WIDE], ids=["narrow", "wide"])
+@pytest.mark.parametrize("scale", [0.0, -0.1, 1.0])
+def test_forced_policy_scales_and_lse(device, pol, scale):
+    q, k, v = inputs(1, 4, 2, 333, 128, seed=5)
+    with policy(pol):
+        out, lse = flash_attention_forward_lse(q.to(device), k.to(device), v.to(device),
+                                               causal=True, scale=scale)
+        torch.cuda.synchronize()
+    check(out, q, k, v, True, scale=scale, label=f"pol{pol} scale{scale}")
+    lse_ref = ref.attention_lse(q.numpy(), k.numpy(), causal=True, scale=scale)
+    np.testing.assert_allclose(lse.cpu().numpy(), lse_ref, atol=2e-4, rtol=1e-5)
+
+
+def test_kernels_agree_and_auto_picks_one(device):
+    """Auto mode equals one of the forced kernels bit for bit, on a size the
+    automatic choice sends to the wide kernel and on one it sends to the
+    narrow kernel."""
+    for (B, Hq, Hkv, N) in ((4, 32, 8, 1000), (1, 4, 4, 300)):
+        q, k, v = (t.to(device) for t in inputs(B, Hq, Hkv, N, 128, seed=B * N))
+        outs = {}
+        for pol in (0, NARROW, WIDE):
+            with policy(pol):
+                outs[pol] = flash_attention_forward(q, k, v, causal=True)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[NARROW]) or torch.equal(outs[0], outs[WIDE])
+        diff = (outs[NARROW].float() - outs[WIDE].float()).abs().max().item()
+        assert diff < 4e-3, diff
