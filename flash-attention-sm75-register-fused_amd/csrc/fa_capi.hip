@@ -80,16 +80,20 @@ int validate(const fa_fwd_params* p, bool fused) {
   if (p->q_stride_n < p->head_dim || p->k_stride_n < p->head_dim ||
       p->v_stride_n < p->head_dim || p->o_stride_n < p->head_dim)
     return fail(FA_ERR_INVALID_ARGUMENT, "row stride must be at least head_dim");
-  if (p->seq_len > (int64_t)fa::fused_block_m() * 65535 || p->seq_len > INT32_MAX / 2)
+  if (p->seq_len > INT32_MAX / 2)
     return fail(FA_ERR_TOO_LARGE, "seq_len %lld exceeds the supported maximum",
                 (long long)p->seq_len);
   // K/V tiles are read through 32-bit buffer windows over one (batch, head).
   if (p->seq_len * p->k_stride_n * 2 > (int64_t)INT32_MAX ||
       p->seq_len * p->v_stride_n * 2 > (int64_t)INT32_MAX)
     return fail(FA_ERR_TOO_LARGE, "seq_len * row stride of K/V exceeds 2^31 bytes");
-  if (p->batch * p->heads_q > (int64_t)(1u << 24))
-    return fail(FA_ERR_TOO_LARGE, "batch*heads_q %lld exceeds 2^24",
-                (long long)(p->batch * p->heads_q));
+  // One 1-D grid of batch*heads_q*ceil(seq_len/128) workgroups of 256
+  // threads; the thread count must stay below 2^32.
+  const int64_t bm = fa::fused_block_m();
+  if (p->batch * p->heads_q > (int64_t)(1u << 24) ||
+      p->batch * p->heads_q * ((p->seq_len + bm - 1) / bm) >= (int64_t)(1u << 24))
+    return fail(FA_ERR_TOO_LARGE, "batch*heads_q*ceil(seq_len/%lld) exceeds 2^24 workgroups",
+                (long long)bm);
   return FA_OK;
 }
 
@@ -107,7 +111,9 @@ fa::FwdArgs make_args(const fa_fwd_params* p) {
   a.n = (int)p->seq_len;
   a.hq = (int)p->heads_q;
   a.group = (int)(p->heads_kv > 0 ? p->heads_q / p->heads_kv : 1);
-  a.num_qblocks = 0;
+  a.num_qblocks = 0;  // grid plan: filled by the launcher
+  a.units = 0;
+  a.xcds = 1;
   const float log2e = 1.4426950408889634f;
   float c = std::fabs(p->scale) * log2e;
   // scale == 0 must still give uniform weights over the visible keys; a tiny

@@ -86,11 +86,9 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const int grp = lane >> 4;  // 16-lane group (transposing reads)
   const int gi = lane & 15;
 
-  const int bh = blockIdx.x;
-  const int b = bh / a.hq;
-  const int hq = bh - b * a.hq;
-  const int hkv = hq / a.group;
-  const int qb = CAUSAL ? (a.num_qblocks - 1 - (int)blockIdx.y) : (int)blockIdx.y;
+  const Work w = block_work(a, (int)blockIdx.x, CAUSAL);
+  const int b = w.b, hq = w.hq, hkv = w.hkv, qb = w.qb;
+  const int bh = b * a.hq + hq;
   const int q0 = qb * kBlockM;
   const int qw = q0 + wave * 32;
   const int qrow = qw + ql;
@@ -445,10 +443,8 @@ int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
                     (policy == 2 || (policy == 0 && kAutoWide &&
                                      (int64_t)batch * a.hq * wide_blocks >= 512));
   if (wide) return launch_fused_forward_wide(a, batch, causal, stream);
-  const int64_t nblocks = ((int64_t)a.n + kBlockM - 1) / kBlockM;
   FwdArgs args = a;
-  args.num_qblocks = (int)nblocks;
-  const dim3 grid((unsigned)(batch * a.hq), (unsigned)nblocks);
+  const dim3 grid((unsigned)plan_grid(args, batch, kBlockM));
 #define FA_LAUNCH(D, C, S) \
   hipLaunchKernelGGL((fa_fwd_kernel<D, C, S>), grid, block, 0, stream, args)
   if (head_dim == 128) {

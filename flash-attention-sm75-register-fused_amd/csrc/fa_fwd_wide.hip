@@ -55,11 +55,9 @@ __global__ void __launch_bounds__(kThreads, 1) fa_fwd_wide_kernel(const FwdArgs 
   const int grp = lane >> 4;
   const int gi = lane & 15;
 
-  const int bh = blockIdx.x;
-  const int b = bh / a.hq;
-  const int hq = bh - b * a.hq;
-  const int hkv = hq / a.group;
-  const int qb = CAUSAL ? (a.num_qblocks - 1 - (int)blockIdx.y) : (int)blockIdx.y;
+  const Work w = block_work(a, (int)blockIdx.x, CAUSAL);
+  const int b = w.b, hq = w.hq, hkv = w.hkv, qb = w.qb;
+  const int bh = b * a.hq + hq;
   const int q0 = qb * kBlockMWide;
   const int qw = q0 + wave * kRowsPerWaveWide;
   const int N = a.n;
@@ -391,10 +389,8 @@ __global__ void __launch_bounds__(kThreads, 1) fa_fwd_wide_kernel(const FwdArgs 
 }  // namespace
 
 int launch_fused_forward_wide(const FwdArgs& a, int batch, bool causal, hipStream_t stream) {
-  const int64_t nblocks = ((int64_t)a.n + kBlockMWide - 1) / kBlockMWide;
   FwdArgs args = a;
-  args.num_qblocks = (int)nblocks;
-  const dim3 grid((unsigned)(batch * a.hq), (unsigned)nblocks);
+  const dim3 grid((unsigned)plan_grid(args, batch, kBlockMWide));
   const dim3 block(kThreads);
   const bool same = a.ksn == a.vsn;
 #define FA_LAUNCH_WIDE(C, S) \

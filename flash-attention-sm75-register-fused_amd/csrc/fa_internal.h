@@ -6,6 +6,10 @@
 
 namespace fa {
 
+// MI355X deals the workgroups of a launch to its 8 XCDs round-robin by
+// linear workgroup id; each XCD has its own L2.
+constexpr int kNumXcds = 8;
+
 // Kernel arguments of the fused forward (passed by value).
 struct FwdArgs {
   const _Float16* q;
@@ -21,6 +25,8 @@ struct FwdArgs {
   int hq;           // query heads
   int group;        // heads_q / heads_kv
   int num_qblocks;  // filled by the launcher
+  int units;        // batch * heads_kv (one unit = one K/V pair of tensors)
+  int xcds;         // 8: units split evenly over the XCDs, else 1 (launcher)
   float c;          // |scale| * log2(e), clamped away from 0
   int negate_q;     // scale < 0: Q fragments are negated (exact in fp16)
 };

@@ -112,5 +112,44 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// Work item of workgroup `wg` of the 1-D grid: batch b, query head hq, KV
+// head hkv and query block qb.  The grid holds units * group * num_qblocks
+// workgroups, a unit being one (batch, KV head).
+//  * Workgroup wg runs on XCD wg % 8.  With a.xcds == 8 (units divisible by
+//    8) XCD x takes the units [x*U/8, (x+1)*U/8), so all query heads of a
+//    group, and all query blocks, that read one K/V pair share an L2.  With
+//    a.xcds == 1 the whole grid is one sequence.
+//  * Within a sequence, workgroups go rank-major: rank r of every head before
+//    rank r+1.  Under causal masking rank 0 is the last (most expensive)
+//    query block, so the cheap blocks fill the tail of the launch.
+struct Work {
+  int b, hq, hkv, qb;
+};
+__device__ __forceinline__ Work block_work(const FwdArgs& a, int wg, bool causal) {
+  const int x = wg % a.xcds;
+  const int p = wg / a.xcds;
+  const int per = a.units / a.xcds;   // units of this sequence
+  const int row = per * a.group;      // workgroups per rank
+  const int rank = p / row;
+  const int rest = p - rank * row;
+  const int ul = rest / a.group;
+  const int u = x * per + ul;
+  const int hkv_count = a.hq / a.group;
+  Work w;
+  w.b = u / hkv_count;
+  w.hkv = u - w.b * hkv_count;
+  w.hq = w.hkv * a.group + (rest - ul * a.group);
+  w.qb = causal ? a.num_qblocks - 1 - rank : rank;
+  return w;
+}
+
+// Host side: fills num_qblocks, units and xcds, returns the 1-D grid size.
+inline int64_t plan_grid(FwdArgs& a, int batch, int block_m) {
+  a.num_qblocks = (int)(((int64_t)a.n + block_m - 1) / block_m);
+  a.units = batch * (a.hq / a.group);
+  a.xcds = a.units % kNumXcds == 0 ? kNumXcds : 1;
+  return (int64_t)batch * a.hq * a.num_qblocks;
+}
+
 }  // namespace
 }  // namespace fa
