@@ -5,7 +5,9 @@
 // src/kernels/flash_attention_forward.cu:345-791 implements for SM75).
 //
 // Work decomposition
-//   grid.x = batch * heads_q, grid.y = query blocks of kBlockM = 128 rows.
+//   A 1-D grid of batch * heads_q * ceil(N / kBlockM) workgroups, kBlockM =
+//   128 query rows each, ordered so the workgroups reading one K/V pair share
+//   an XCD (block_work in fa_kernel_common.h).
 //   One workgroup = 4 waves; wave w owns query rows [q0 + 32w, q0 + 32w + 32).
 //   Key/value rows stream through LDS in tiles of kBlockN = 64 keys.  Tiles
 //   go straight from HBM to LDS (buffer_load ... lds: lane l's 16 bytes land
