@@ -6,8 +6,9 @@
 //   flash_attention_forward_scalar, flash_attention_forward_wmma_qk,
 // each (Tensor Q, Tensor K, Tensor V, bool causal, float scale) -> Tensor.
 // Additions: flash_attention_forward accepts grouped K/V heads (Hkv divides
-// Hq) so no repeat_interleave copy is needed, and flash_attention_forward_lse
-// also returns the fp32 row log-sum-exp.
+// Hq) so no repeat_interleave copy is needed, flash_attention_forward_lse
+// also returns the fp32 row log-sum-exp, and flash_attention_forward_ex takes
+// strided views in place, Nq != Nk and either causal alignment.
 //
 // All checks run before any device work; the kernels are enqueued on the
 // current HIP stream of Q's device and the host is not blocked.
@@ -107,6 +108,88 @@ std::tuple<torch::Tensor, torch::Tensor> flash_attention_forward_lse(
   return {O, L};
 }
 
+// ---- flash_attention_forward_ex: strided views, Nq != Nk, causal alignment --
+
+// Whether the kernels can read t in place: head_dim contiguous, the other
+// strides multiples of 8 elements, a 16-byte aligned base and (for K/V) a
+// (batch, head) slice that fits the 32-bit buffer window.  Strides of size-1
+// dimensions never matter and are ignored.
+bool kernel_layout_ok(const torch::Tensor& t, bool kv) {
+  if (t.stride(3) != 1) return false;
+  if ((reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) != 0) return false;
+  for (int i = 0; i < 3; ++i)
+    if (t.size(i) > 1 && (t.stride(i) < 0 || t.stride(i) % 8 != 0)) return false;
+  if (t.size(2) > 1 && t.stride(2) < t.size(3)) return false;
+  if (kv && t.size(2) * (t.size(2) > 1 ? t.stride(2) : t.size(3)) * 2 > (int64_t)INT32_MAX)
+    return false;
+  return true;
+}
+
+torch::Tensor kernel_view(const torch::Tensor& t, bool kv) {
+  return kernel_layout_ok(t, kv) ? t : t.contiguous();
+}
+
+// Stride of dimension i, or `fallback` for a size-1 dimension.
+int64_t eff_stride(const torch::Tensor& t, int i, int64_t fallback) {
+  return t.size(i) == 1 ? fallback : t.stride(i);
+}
+
+std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_ex(
+    torch::Tensor Q, torch::Tensor K, torch::Tensor V, int64_t causal, double scale,
+    bool return_lse) {
+  for (auto* pr : {&Q, &K, &V}) {
+    const torch::Tensor& t = *pr;
+    TORCH_CHECK(t.is_cuda(), "inputs must be CUDA tensors");
+    TORCH_CHECK(t.dtype() == torch::kFloat16, "inputs must be FP16");
+    TORCH_CHECK(t.dim() == 4, "inputs must be [B, H, N, D]");
+  }
+  check_same_device(Q, K, V);
+  TORCH_CHECK(Q.size(0) == K.size(0), "batch mismatch");
+  TORCH_CHECK(K.size(1) > 0 && Q.size(1) % K.size(1) == 0, "heads mismatch: Q heads (",
+              Q.size(1), ") not divisible by K/V heads (", K.size(1), ")");
+  TORCH_CHECK(Q.size(3) == K.size(3), "head_dim mismatch");
+  TORCH_CHECK(K.sizes() == V.sizes(), "K and V must have identical shapes");
+  TORCH_CHECK(causal >= 0 && causal <= 2,
+              "causal must be 0 (none), 1 (top-left) or 2 (bottom-right), got ", causal);
+  const auto D = Q.size(3);
+  TORCH_CHECK(D == 64 || D == 128, "flash_attention_forward supports head_dim=64 or 128, got ", D);
+  Q = kernel_view(Q, false);
+  K = kernel_view(K, true);
+  V = kernel_view(V, true);
+  auto O = torch::empty_like(Q);  // keeps Q's dense layout (e.g. [B, N, H, D] storage)
+  if (!kernel_layout_ok(O, false)) O = torch::empty(Q.sizes(), Q.options());
+  c10::optional<torch::Tensor> L;
+  if (return_lse)
+    L = torch::empty({Q.size(0), Q.size(1), Q.size(2)}, Q.options().dtype(torch::kFloat32));
+  if (Q.numel() == 0) return {O, L};
+  TORCH_CHECK(K.size(2) > 0, "K/V must hold at least one row");
+  const at::OptionalDeviceGuard guard(at::device_of(Q));
+  fa_fwd_params p{};
+  p.q = reinterpret_cast<const fa_half*>(Q.data_ptr<at::Half>());
+  p.k = reinterpret_cast<const fa_half*>(K.data_ptr<at::Half>());
+  p.v = reinterpret_cast<const fa_half*>(V.data_ptr<at::Half>());
+  p.o = reinterpret_cast<fa_half*>(O.data_ptr<at::Half>());
+  p.lse = return_lse ? L->data_ptr<float>() : nullptr;
+  p.batch = Q.size(0);
+  p.heads_q = Q.size(1);
+  p.heads_kv = K.size(1);
+  p.seq_len = Q.size(2);
+  p.seq_len_kv = K.size(2);
+  p.head_dim = D;
+  const int64_t qn = eff_stride(Q, 2, D), kn = eff_stride(K, 2, D), vn = eff_stride(V, 2, D),
+                on = eff_stride(O, 2, D);
+  p.q_stride_n = qn; p.q_stride_h = eff_stride(Q, 1, 0); p.q_stride_b = eff_stride(Q, 0, 0);
+  p.k_stride_n = kn; p.k_stride_h = eff_stride(K, 1, 0); p.k_stride_b = eff_stride(K, 0, 0);
+  p.v_stride_n = vn; p.v_stride_h = eff_stride(V, 1, 0); p.v_stride_b = eff_stride(V, 0, 0);
+  p.o_stride_n = on; p.o_stride_h = eff_stride(O, 1, 0); p.o_stride_b = eff_stride(O, 0, 0);
+  p.scale = (float)scale;
+  p.causal = (int)causal;
+  p.stream = c10::hip::getCurrentHIPStream(Q.device().index()).stream();
+  const int st = fa_sm75_forward(&p);
+  TORCH_CHECK(st == FA_OK, "flash_attention_forward_ex: ", fa_sm75_last_error());
+  return {O, L};
+}
+
 torch::Tensor d64_compat(const char* tag, torch::Tensor Q, torch::Tensor K,
                          torch::Tensor V, bool causal, float scale) {
   check_tensor(Q, "Q");
@@ -162,5 +245,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("flash_attention_forward_scalar", &flash_attention_forward_scalar);
   m.def("flash_attention_forward_wmma_qk", &flash_attention_forward_wmma_qk);
   m.def("flash_attention_forward_lse", &flash_attention_forward_lse);
+  m.def("flash_attention_forward_ex", &flash_attention_forward_ex,
+        "O (and optionally the fp32 row LSE) for Q [B,Hq,Nq,D], K/V [B,Hkv,Nk,D]; "
+        "strided views read in place; causal 0 none, 1 top-left, 2 bottom-right",
+        pybind11::arg("Q"), pybind11::arg("K"), pybind11::arg("V"), pybind11::arg("causal"),
+        pybind11::arg("scale"), pybind11::arg("return_lse") = false);
   m.def("abi_version", []() { return fa_sm75_abi_version(); });
 }

@@ -31,11 +31,16 @@ int fail(int status, const char* fmt, ...) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Key/value rows of a call (seq_len_kv == 0 selects seq_len).
+int64_t kv_rows(const fa_fwd_params* p) {
+  return p->seq_len_kv != 0 ? p->seq_len_kv : p->seq_len;
+}
+
 // Shared validation of the fused and naive entry points.
 int validate(const fa_fwd_params* p, bool fused) {
   if (p == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "params must not be NULL");
   if (p->batch < 0 || p->heads_q < 0 || p->heads_kv < 0 || p->seq_len < 0 ||
-      p->head_dim < 0)
+      p->head_dim < 0 || p->seq_len_kv < 0)
     return fail(FA_ERR_INVALID_ARGUMENT,
                 "sizes must be non-negative (batch=%lld heads_q=%lld heads_kv=%lld "
                 "seq_len=%lld head_dim=%lld)",
@@ -60,6 +65,11 @@ int validate(const fa_fwd_params* p, bool fused) {
                 (long long)p->heads_q, (long long)p->heads_kv);
   if (!std::isfinite(p->scale))
     return fail(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  if (p->causal < FA_CAUSAL_NONE || p->causal > FA_CAUSAL_BOTTOM_RIGHT)
+    return fail(FA_ERR_INVALID_ARGUMENT, "causal must be 0, 1 (top-left) or 2 (bottom-right), got %d",
+                p->causal);
+  if (!fused && p->seq_len_kv != 0 && p->seq_len_kv != p->seq_len)
+    return fail(FA_ERR_INVALID_ARGUMENT, "naive path needs seq_len_kv == seq_len");
   const bool empty = p->batch == 0 || p->heads_q == 0 || p->seq_len == 0;
   if (empty) return FA_OK;
   if (!p->q || !p->k || !p->v || !p->o)
@@ -80,13 +90,14 @@ int validate(const fa_fwd_params* p, bool fused) {
   if (p->q_stride_n < p->head_dim || p->k_stride_n < p->head_dim ||
       p->v_stride_n < p->head_dim || p->o_stride_n < p->head_dim)
     return fail(FA_ERR_INVALID_ARGUMENT, "row stride must be at least head_dim");
-  if (p->seq_len > INT32_MAX / 2)
-    return fail(FA_ERR_TOO_LARGE, "seq_len %lld exceeds the supported maximum",
-                (long long)p->seq_len);
+  const int64_t nk = kv_rows(p);
+  if (p->seq_len > INT32_MAX / 2 || nk > INT32_MAX / 2)
+    return fail(FA_ERR_TOO_LARGE, "seq_len %lld / seq_len_kv %lld exceeds the supported maximum",
+                (long long)p->seq_len, (long long)nk);
   // K/V tiles are read through 32-bit buffer windows over one (batch, head).
-  if (p->seq_len * p->k_stride_n * 2 > (int64_t)INT32_MAX ||
-      p->seq_len * p->v_stride_n * 2 > (int64_t)INT32_MAX)
-    return fail(FA_ERR_TOO_LARGE, "seq_len * row stride of K/V exceeds 2^31 bytes");
+  if (nk * p->k_stride_n * 2 > (int64_t)INT32_MAX ||
+      nk * p->v_stride_n * 2 > (int64_t)INT32_MAX)
+    return fail(FA_ERR_TOO_LARGE, "seq_len_kv * row stride of K/V exceeds 2^31 bytes");
   // One 1-D grid of batch*heads_q*ceil(seq_len/128) workgroups of 256
   // threads; the thread count must stay below 2^32.
   const int64_t bm = fa::fused_block_m();
@@ -109,6 +120,8 @@ fa::FwdArgs make_args(const fa_fwd_params* p) {
   a.vsb = p->v_stride_b; a.vsh = p->v_stride_h; a.vsn = p->v_stride_n;
   a.osb = p->o_stride_b; a.osh = p->o_stride_h; a.osn = p->o_stride_n;
   a.n = (int)p->seq_len;
+  a.nk = (int)kv_rows(p);
+  a.diag = p->causal == FA_CAUSAL_BOTTOM_RIGHT ? a.nk - a.n : 0;
   a.hq = (int)p->heads_q;
   a.group = (int)(p->heads_kv > 0 ? p->heads_q / p->heads_kv : 1);
   a.num_qblocks = 0;  // grid plan: filled by the launcher
@@ -163,11 +176,11 @@ void legacy_launch(const char* tag, const fa_half* Q, const fa_half* K, const fa
 extern "C" {
 
 void fa_sm75_set_contiguous_strides(fa_fwd_params* p) {
-  const int64_t D = p->head_dim, N = p->seq_len;
+  const int64_t D = p->head_dim, N = p->seq_len, Nk = kv_rows(p);
   p->q_stride_n = D; p->q_stride_h = N * D; p->q_stride_b = p->heads_q * N * D;
   p->o_stride_n = D; p->o_stride_h = N * D; p->o_stride_b = p->heads_q * N * D;
-  p->k_stride_n = D; p->k_stride_h = N * D; p->k_stride_b = p->heads_kv * N * D;
-  p->v_stride_n = D; p->v_stride_h = N * D; p->v_stride_b = p->heads_kv * N * D;
+  p->k_stride_n = D; p->k_stride_h = Nk * D; p->k_stride_b = p->heads_kv * Nk * D;
+  p->v_stride_n = D; p->v_stride_h = Nk * D; p->v_stride_b = p->heads_kv * Nk * D;
 }
 
 int fa_sm75_forward(const fa_fwd_params* p) {

@@ -94,7 +94,8 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const int q0 = qb * kBlockM;
   const int qw = q0 + wave * 32;
   const int qrow = qw + ql;
-  const int N = a.n;
+  const int N = a.n;    // query rows
+  const int NK = a.nk;  // key rows
 
   const _Float16* Qp = a.q + b * a.qsb + hq * a.qsh;
   const _Float16* Kp = a.k + b * a.ksb + hkv * a.ksh;
@@ -115,7 +116,8 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
     for (int kk = 0; kk < KK; ++kk) qf[kk] = -qf[kk];
   }
 
-  const int kv_len = CAUSAL ? min(N, q0 + kBlockM) : N;
+  // Keys this block can see (none for a block entirely before the diagonal).
+  const int kv_len = CAUSAL ? max(0, min(NK, q0 + kBlockM + a.diag)) : NK;
   const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
 
   // Direct-load map: wave w fills 1 KB segments w, w + 4, ...; lane l of a
@@ -139,8 +141,8 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   }
   const int k_tile_bytes = (int)(kBlockN * a.ksn * 2);
   const int v_tile_bytes = (int)(kBlockN * a.vsn * 2);
-  const int k_all_bytes = (int)(N * a.ksn * 2);
-  const int v_all_bytes = (int)(N * a.vsn * 2);
+  const int k_all_bytes = (int)(NK * a.ksn * 2);
+  const int v_all_bytes = (int)(NK * a.vsn * 2);
 
   // Buffer selection by compile-time parity.
   auto kbuf = [&](auto par) -> _Float16* {
@@ -229,14 +231,15 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   // more than 2^kRescaleLog2 (rescaling O and l), and sets mc.
   auto prepare = [&](int j, float16v (&s)[2], float mx) {
     const int kstart = j * kBlockN;
-    const bool need_mask = (kstart + kBlockN > N) || (CAUSAL && kstart + kBlockN - 1 > qw);
+    const bool need_mask =
+        (kstart + kBlockN > NK) || (CAUSAL && kstart + kBlockN - 1 > qw + a.diag);
     if (need_mask) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
-          const bool masked = (key >= N) || (CAUSAL && key > qrow);
+          const bool masked = (key >= NK) || (CAUSAL && key > qrow + a.diag);
           if (masked) s[t][i] = -__builtin_inff();
         }
       }

@@ -60,7 +60,8 @@ __global__ void __launch_bounds__(kThreads, 1) fa_fwd_wide_kernel(const FwdArgs 
   const int bh = b * a.hq + hq;
   const int q0 = qb * kBlockMWide;
   const int qw = q0 + wave * kRowsPerWaveWide;
-  const int N = a.n;
+  const int N = a.n;    // query rows
+  const int NK = a.nk;  // key rows
   int qrow[2];
   qrow[0] = qw + ql;
   qrow[1] = qw + 32 + ql;
@@ -70,7 +71,7 @@ __global__ void __launch_bounds__(kThreads, 1) fa_fwd_wide_kernel(const FwdArgs 
   const _Float16* Vp = a.v + b * a.vsb + hkv * a.vsh;
   _Float16* q_mine = q_lds + wave * QTILE;
 
-  const int kv_len = CAUSAL ? min(N, q0 + kBlockMWide) : N;
+  const int kv_len = CAUSAL ? max(0, min(NK, q0 + kBlockMWide + a.diag)) : NK;
   const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
 
   // ---- direct-load maps (see Lds): tiles are filled by 1 KB segments ------
@@ -91,8 +92,8 @@ __global__ void __launch_bounds__(kThreads, 1) fa_fwd_wide_kernel(const FwdArgs 
   }
   const int k_tile_bytes = (int)(kBlockN * a.ksn * 2);
   const int v_tile_bytes = (int)(kBlockN * a.vsn * 2);
-  const int k_all_bytes = (int)(N * a.ksn * 2);
-  const int v_all_bytes = (int)(N * a.vsn * 2);
+  const int k_all_bytes = (int)(NK * a.ksn * 2);
+  const int v_all_bytes = (int)(NK * a.vsn * 2);
 
   auto kbuf = [&](auto par) -> _Float16* {
     if constexpr (decltype(par)::value) return k_lds1; else return k_lds0;
@@ -192,14 +193,14 @@ __global__ void __launch_bounds__(kThreads, 1) fa_fwd_wide_kernel(const FwdArgs 
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const bool need_mask =
-          (kstart + kBlockN > N) || (CAUSAL && kstart + kBlockN - 1 > qw + 32 * c);
+          (kstart + kBlockN > NK) || (CAUSAL && kstart + kBlockN - 1 > qw + 32 * c + a.diag);
       if (need_mask) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
-            const bool masked = (key >= N) || (CAUSAL && key > qrow[c]);
+            const bool masked = (key >= NK) || (CAUSAL && key > qrow[c] + a.diag);
             if (masked) s_cur[c][t][i] = -__builtin_inff();
           }
         }

@@ -21,7 +21,9 @@ struct FwdArgs {
   int64_t ksb, ksh, ksn;
   int64_t vsb, vsh, vsn;
   int64_t osb, osh, osn;
-  int n;            // sequence length (queries == keys)
+  int n;            // query rows
+  int nk;           // key/value rows
+  int diag;         // causal: key j visible to query i iff j <= i + diag
   int hq;           // query heads
   int group;        // heads_q / heads_kv
   int num_qblocks;  // filled by the launcher

@@ -106,3 +106,42 @@ def flash_attention_forward_lse(Q, K, V, causal=False, scale=None):
     return _C.flash_attention_forward_lse(
         Q.contiguous(), K.contiguous(), V.contiguous(), bool(causal), float(scale)
     )
+
+
+_CAUSAL_CODES = {False: 0, True: 1, "top_left": 1, "bottom_right": 2}
+
+
+def flash_attention_forward_ex(Q, K, V, causal=False, scale=None, return_lse=False):
+    """Forward over separate query/key lengths and strided views.
+
+    No reference counterpart: the reference binding requires Nq == Nk and
+    contiguous tensors (reference pytorch_extension.cpp:22-25,61).
+
+    Args:
+        Q: [B, H_q, N_q, D] float16 on the GPU; any layout whose head_dim is
+           contiguous and whose other strides are multiples of 8 is read in
+           place (e.g. a [B, N, H, D] buffer viewed as [B, H, N, D]), other
+           layouts are copied first.
+        K, V: [B, H_kv, N_k, D] float16, H_kv divides H_q.
+        causal: False; True or "top_left" (key j visible to query i iff
+            j <= i, torch SDPA's is_causal); "bottom_right" (iff
+            j <= i + N_k - N_q).  A query that sees no key gets a zero row.
+        scale: softmax scale (default 1/sqrt(D)).
+        return_lse: also return the fp32 natural-log row LSE [B, H_q, N_q].
+
+    Returns:
+        O [B, H_q, N_q, D] float16 with Q's memory layout when Q is dense,
+        or (O, LSE) when return_lse.
+    """
+    head_dim = _check_inputs(Q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    try:
+        code = _CAUSAL_CODES[causal]
+    except (KeyError, TypeError):
+        raise ValueError(
+            f"causal must be False, True, 'top_left' or 'bottom_right', got {causal!r}"
+        ) from None
+    _check_gqa_heads(Q, K)
+    o, lse = _C.flash_attention_forward_ex(Q, K, V, code, float(scale), bool(return_lse))
+    return (o, lse) if return_lse else o

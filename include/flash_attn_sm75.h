@@ -3,7 +3,8 @@
  *
  * Plain pointers and sizes only: no torch, no HIP types in the signatures.
  * Every tensor is IEEE binary16 (`fa_half`, the bit pattern of CUDA's `half`)
- * laid out [batch, heads, seq_len, head_dim] with head_dim contiguous.
+ * laid out [batch, heads, seq_len, head_dim] with head_dim contiguous (K and V
+ * may hold a different number of rows, seq_len_kv, in fa_sm75_forward).
  *
  * Two groups of entry points:
  *
@@ -47,14 +48,25 @@ enum fa_status {
   FA_ERR_HIP = 6                   /* HIP runtime error (see message) */
 };
 
+/* Values of fa_fwd_params.causal. */
+enum fa_causal {
+  FA_CAUSAL_NONE = 0,
+  FA_CAUSAL_TOP_LEFT = 1,     /* key j visible to query i iff j <= i (the reference's
+                                 causal flag; torch SDPA's is_causal) */
+  FA_CAUSAL_BOTTOM_RIGHT = 2  /* iff j <= i + seq_len_kv - seq_len (queries are the
+                                 last seq_len positions of the keys' sequence) */
+};
+
 /* Arguments of one forward call.  Strides are in elements; the last
- * (head_dim) dimension must be contiguous. */
+ * (head_dim) dimension must be contiguous.  N = seq_len query rows,
+ * Nk = seq_len_kv key rows (0 selects Nk = N). */
 typedef struct fa_fwd_params {
-  const fa_half* q;  /* [B, Hq,  N, D] */
-  const fa_half* k;  /* [B, Hkv, N, D] */
-  const fa_half* v;  /* [B, Hkv, N, D] */
-  fa_half* o;        /* [B, Hq,  N, D] output */
-  float* lse;        /* optional [B, Hq, N] fp32 natural-log row LSE, or NULL */
+  const fa_half* q;  /* [B, Hq,  N,  D] */
+  const fa_half* k;  /* [B, Hkv, Nk, D] */
+  const fa_half* v;  /* [B, Hkv, Nk, D] */
+  fa_half* o;        /* [B, Hq,  N,  D] output */
+  float* lse;        /* optional [B, Hq, N] fp32 natural-log row LSE, or NULL;
+                        -inf for a row that sees no key (its O row is 0) */
   int64_t batch;
   int64_t heads_q;
   int64_t heads_kv;
@@ -65,11 +77,12 @@ typedef struct fa_fwd_params {
   int64_t v_stride_b, v_stride_h, v_stride_n;
   int64_t o_stride_b, o_stride_h, o_stride_n;
   float scale;       /* softmax scale applied to Q.K (reference default 1/sqrt(D)) */
-  int causal;        /* nonzero: key j is visible to query i iff j <= i */
+  int causal;        /* an fa_causal value */
   void* stream;      /* hipStream_t; NULL selects the default stream */
+  int64_t seq_len_kv; /* key/value rows Nk; 0 means Nk = seq_len */
 } fa_fwd_params;
 
-/* Fills strides for contiguous [B,H,N,D] tensors. */
+/* Fills strides for contiguous [B,H,N,D] Q/O and [B,Hkv,Nk,D] K/V tensors. */
 void fa_sm75_set_contiguous_strides(fa_fwd_params* p);
 
 /* Fused MFMA forward.  Replaces the launch in reference
@@ -81,7 +94,8 @@ int fa_sm75_forward(const fa_fwd_params* p);
 /* Three-pass reference-style path (QK^T -> row softmax -> PV) through an fp32
  * score workspace of batch*heads_q*seq_len*seq_len floats.  Replaces reference
  * src/kernels/naive_attention.cu:115-164.  Any head_dim that is a multiple of 8
- * (1..256) is accepted.  Asynchronous on p->stream. */
+ * (1..256) is accepted; seq_len_kv must be 0 or seq_len.  Asynchronous on
+ * p->stream. */
 int fa_sm75_naive_forward(const fa_fwd_params* p, float* workspace);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -101,7 +115,7 @@ int fa_sm75_abi_version(void);
 enum fa_kernel_policy { FA_POLICY_AUTO = 0, FA_POLICY_NARROW = 1, FA_POLICY_WIDE = 2 };
 int fa_sm75_set_kernel_policy(int policy); /* FA_OK or FA_ERR_INVALID_ARGUMENT */
 int fa_sm75_get_kernel_policy(void);
-#define FA_SM75_ABI_VERSION 1
+#define FA_SM75_ABI_VERSION 2
 
 /* ---- Reference launcher signatures ------------------------------------ */
 

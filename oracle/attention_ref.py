@@ -37,11 +37,36 @@ def expand_kv_for_gqa(Q: np.ndarray, K: np.ndarray, V: np.ndarray):
     return np.repeat(K, f, axis=1), np.repeat(V, f, axis=1)
 
 
+def causal_mask(nq: int, nk: int, causal, row0: int = 0, rows: int | None = None):
+    """Boolean [rows, nk] mask of the *hidden* keys of query rows row0.., or None.
+
+    causal = False/0: nothing hidden.  True/1 (top-left): key j hidden from
+    query i iff j > i -- the reference's triu(diagonal=1) (attention_ref.py:
+    34-40) for nq == nk, and torch SDPA's is_causal for nq != nk.  2
+    (bottom-right): iff j > i + nk - nq, the queries being the last nq
+    positions of the keys' sequence.  Both agree when nq == nk.
+    """
+    if not causal:
+        return None
+    if rows is None:
+        rows = nq - row0
+    diag = nk - nq if int(causal) == 2 else 0
+    cols = np.arange(nk)[None, :]
+    rws = np.arange(row0, row0 + rows)[:, None]
+    return cols > rws + diag
+
+
 def _softmax_rows_f32(S: np.ndarray) -> np.ndarray:
-    """torch.softmax(S, dim=-1) in fp32: exp(S - rowmax) / rowsum."""
+    """torch.softmax(S, dim=-1) in fp32: exp(S - rowmax) / rowsum.
+
+    A row with every key hidden gives 0 (the kernels' l == 0 -> 1/l = 0 rule,
+    reference flash_attention_forward.cu:562), not NaN.
+    """
     m = S.max(axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, np.float32(0))
     E = np.exp(S - m, dtype=np.float32)
-    return E / E.sum(axis=-1, keepdims=True, dtype=np.float32)
+    tot = E.sum(axis=-1, keepdims=True, dtype=np.float32)
+    return E / np.where(tot > 0, tot, np.float32(1))
 
 
 def attention_reference(Q, K, V, causal=False, scale=None, return_f32=False):
@@ -62,9 +87,8 @@ def attention_reference(Q, K, V, causal=False, scale=None, return_f32=False):
     kf = K.astype(np.float32)
     vf = V.astype(np.float32)
     S = np.matmul(qf, np.swapaxes(kf, -1, -2)) * np.float32(scale)
-    if causal:
-        n = Q.shape[-2]
-        mask = np.triu(np.ones((n, n), dtype=bool), k=1)
+    mask = causal_mask(Q.shape[-2], K.shape[-2], causal)
+    if mask is not None:
         S[..., mask] = -np.inf
     P = _softmax_rows_f32(S)
     O = np.matmul(P, vf)
@@ -85,7 +109,7 @@ def attention_reference_chunked(Q, K, V, causal=False, scale=None, rows=512,
     K = np.asarray(K)
     V = np.asarray(V)
     B, Hq, N, D = Q.shape
-    Hkv = K.shape[1]
+    Hkv, Nk = K.shape[1], K.shape[2]
     if Hkv == 0 or Hq % Hkv != 0:
         raise RuntimeError(
             f"GQA expansion: Q heads ({Hq}) not divisible by K/V heads ({Hkv})"
@@ -105,10 +129,9 @@ def attention_reference_chunked(Q, K, V, causal=False, scale=None, rows=512,
                 r1 = min(N, r0 + rows)
                 qf = Q[b, h, r0:r1].astype(np.float32)
                 S = (qf @ kt) * sc
-                if causal:
-                    cols = np.arange(N)[None, :]
-                    rws = np.arange(r0, r1)[:, None]
-                    S[cols > rws] = -np.inf
+                mask = causal_mask(N, Nk, causal, r0, r1 - r0)
+                if mask is not None:
+                    S[mask] = -np.inf
                 P = _softmax_rows_f32(S)
                 o = P @ vf
                 out[b, oi, r0:r1] = o if return_f32 else o.astype(np.float16)
@@ -133,10 +156,13 @@ def attention_lse(Q, K, causal=False, scale=None, dtype=np.float64):
             q = Q[b, h].astype(dtype)
             k = K[b, h // group].astype(dtype)
             S = (q @ k.T) * dtype(scale)
-            if causal:
-                S[np.triu(np.ones((N, N), dtype=bool), k=1)] = -np.inf
+            mask = causal_mask(N, K.shape[2], causal)
+            if mask is not None:
+                S[mask] = -np.inf
             m = S.max(axis=-1, keepdims=True)
-            out[b, h] = (m[:, 0] + np.log(np.exp(S - m).sum(axis=-1)))
+            m = np.where(np.isfinite(m), m, 0)
+            with np.errstate(divide="ignore"):
+                out[b, h] = (m[:, 0] + np.log(np.exp(S - m).sum(axis=-1)))
     return out
 
 
@@ -150,13 +176,14 @@ def attention_f64(Q, K, V, causal=False, scale=None):
     k = K.astype(np.float64)
     v = V.astype(np.float64)
     S = np.matmul(q, np.swapaxes(k, -1, -2)) * float(scale)
-    if causal:
-        n = Q.shape[-2]
-        S[..., np.triu(np.ones((n, n), dtype=bool), k=1)] = -np.inf
+    mask = causal_mask(Q.shape[-2], K.shape[-2], causal)
+    if mask is not None:
+        S[..., mask] = -np.inf
     m = S.max(axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
     E = np.exp(S - m)
-    P = E / E.sum(axis=-1, keepdims=True)
-    return np.matmul(P, v)
+    tot = E.sum(axis=-1, keepdims=True)
+    return np.matmul(E / np.where(tot > 0, tot, 1.0), v)
 
 
 def check_correctness(output, reference, name="", atol=1e-2, rtol=1e-2):

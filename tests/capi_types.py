@@ -18,4 +18,8 @@ class Params(ctypes.Structure):
         ("v_stride_b", ctypes.c_int64), ("v_stride_h", ctypes.c_int64), ("v_stride_n", ctypes.c_int64),
         ("o_stride_b", ctypes.c_int64), ("o_stride_h", ctypes.c_int64), ("o_stride_n", ctypes.c_int64),
         ("scale", ctypes.c_float), ("causal", ctypes.c_int), ("stream", ctypes.c_void_p),
+        ("seq_len_kv", ctypes.c_int64),
     ]]
+
+
+FA_CAUSAL_NONE, FA_CAUSAL_TOP_LEFT, FA_CAUSAL_BOTTOM_RIGHT = 0, 1, 2

@@ -76,6 +76,17 @@ def test_contiguous_strides(lib):
     assert (p.k_stride_n, p.k_stride_h, p.k_stride_b) == (128, 64 * 128, 2 * 64 * 128)
 
 
+def test_contiguous_strides_separate_kv_length(lib):
+    p = Params()
+    p.batch, p.heads_q, p.heads_kv, p.seq_len, p.head_dim = 2, 4, 2, 5, 64
+    p.seq_len_kv = 300
+    lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+    assert (p.q_stride_n, p.q_stride_h, p.q_stride_b) == (64, 5 * 64, 4 * 5 * 64)
+    assert (p.o_stride_n, p.o_stride_h, p.o_stride_b) == (64, 5 * 64, 4 * 5 * 64)
+    assert (p.k_stride_n, p.k_stride_h, p.k_stride_b) == (64, 300 * 64, 2 * 300 * 64)
+    assert (p.v_stride_n, p.v_stride_h, p.v_stride_b) == (64, 300 * 64, 2 * 300 * 64)
+
+
 @pytest.mark.parametrize("kw,status,msg", [
     (dict(head_dim=96), 2, b"supports head_dim=64 or 128, got 96"),
     (dict(heads_kv=3), 3, b"not divisible"),
@@ -85,6 +96,10 @@ def test_contiguous_strides(lib):
     (dict(k=0x10008), 4, b"16-byte aligned"),
     (dict(q_stride_n=100), 4, b"multiples of 8"),
     (dict(scale=float("inf")), 1, b"finite"),
+    (dict(causal=3), 1, b"causal must be 0, 1 (top-left) or 2 (bottom-right)"),
+    (dict(causal=-1), 1, b"causal must be"),
+    (dict(seq_len_kv=-5), 1, b"non-negative"),
+    (dict(seq_len_kv=1 << 30), 5, b"exceeds the supported maximum"),
 ])
 def test_validation_errors(lib, kw, status, msg):
     p = make(lib, **kw)
@@ -108,10 +123,13 @@ def test_naive_validation(lib):
     p2 = make(lib, head_dim=100)
     assert lib.fa_sm75_naive_forward(ctypes.byref(p), None) == 1  # workspace NULL
     assert lib.fa_sm75_naive_forward(ctypes.byref(p2), None) == 2  # not a multiple of 8
+    p3 = make(lib, seq_len_kv=65)
+    assert lib.fa_sm75_naive_forward(ctypes.byref(p3), ctypes.c_void_p(0x10000)) == 1
+    assert b"seq_len_kv == seq_len" in lib.fa_sm75_last_error()
 
 
 def test_abi_version(lib):
-    assert lib.fa_sm75_abi_version() == 1
+    assert lib.fa_sm75_abi_version() == 2
 
 
 def test_kernel_policy_switch(lib):

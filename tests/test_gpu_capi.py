@@ -108,3 +108,25 @@ def test_legacy_launcher_rejects_bad_head_dim(device, lib, capfd):
     err = capfd.readouterr().err
     assert "head_dim=64 or 128" in err
     assert torch.all(o == 3.0)  # untouched, as the reference launcher leaves it
+
+
+@pytest.mark.parametrize("causal", [0, 1, 2])
+def test_separate_kv_length_matches_binding(device, lib, causal):
+    """fa_sm75_forward with seq_len_kv != seq_len gives the binding's bytes."""
+    B, H, Hkv, Nq, Nk, D = 2, 4, 2, 50, 211, 64
+    g = torch.Generator("cpu").manual_seed(30 + causal)
+    q = torch.randn(B, H, Nq, D, generator=g).half().to(device)
+    k = torch.randn(B, Hkv, Nk, D, generator=g).half().to(device)
+    v = torch.randn(B, Hkv, Nk, D, generator=g).half().to(device)
+    o = torch.empty_like(q)
+    p = Params()
+    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    p.batch, p.heads_q, p.heads_kv, p.seq_len, p.head_dim = B, H, Hkv, Nq, D
+    p.seq_len_kv = Nk
+    lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+    p.scale, p.causal = 0.125, causal
+    p.stream = torch.cuda.current_stream().cuda_stream
+    assert lib.fa_sm75_forward(ctypes.byref(p)) == 0, lib.fa_sm75_last_error()
+    expect = _C.flash_attention_forward_ex(q, k, v, causal, 0.125, False)[0]
+    torch.cuda.synchronize()
+    assert torch.equal(o, expect)

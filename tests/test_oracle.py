@@ -242,3 +242,86 @@ def test_flops_formula():
     # C4: B=1 Hq=32 N=8192 d=128 causal
     assert ref.flops(1, 32, 8192, 128, causal=True) == 549755813888
     assert ref.flops(4, 12, 1024, 64) == 12884901888
+
+
+# ---- separate query / key lengths (no reference counterpart: the reference
+# binding rejects Nq != Nk).  Pinned against the square-causal oracle above
+# and against torch's CPU scaled_dot_product_attention. -----------------------
+
+def test_causal_mask_alignments():
+    assert np.array_equal(ref.causal_mask(5, 5, True), np.triu(np.ones((5, 5), bool), 1))
+    assert np.array_equal(ref.causal_mask(5, 5, 2), ref.causal_mask(5, 5, 1))
+    assert ref.causal_mask(3, 7, False) is None
+    tl = ref.causal_mask(2, 4, 1)
+    br = ref.causal_mask(2, 4, 2)
+    assert tl.tolist() == [[False, True, True, True], [False, False, True, True]]
+    assert br.tolist() == [[False, False, False, True], [False, False, False, False]]
+    # a row block of the full mask
+    assert np.array_equal(ref.causal_mask(9, 12, 2, row0=3, rows=4),
+                          ref.causal_mask(9, 12, 2)[3:7])
+
+
+def test_top_left_with_longer_keys_equals_truncated_keys():
+    q = rnd((1, 4, 24, 64), 31)
+    k = rnd((1, 2, 70, 64), 32)
+    v = rnd((1, 2, 70, 64), 33)
+    got = ref.attention_reference(q, k, v, causal=1, return_f32=True)
+    want = ref.attention_reference(q, k[:, :, :24], v[:, :, :24], causal=True, return_f32=True)
+    np.testing.assert_allclose(got, want, atol=1e-6)
+
+
+def test_bottom_right_is_tail_of_square_causal():
+    n_k, n_q = 90, 13
+    qf = rnd((2, 2, n_k, 128), 34)
+    k = rnd((2, 1, n_k, 128), 35)
+    v = rnd((2, 1, n_k, 128), 36)
+    full = ref.attention_reference(qf, k, v, causal=True, return_f32=True)
+    got = ref.attention_reference(qf[:, :, n_k - n_q:], k, v, causal=2, return_f32=True)
+    np.testing.assert_allclose(got, full[:, :, n_k - n_q:], atol=1e-6)
+    lse_full = ref.attention_lse(qf, k, causal=True)
+    lse = ref.attention_lse(qf[:, :, n_k - n_q:], k, causal=2)
+    np.testing.assert_allclose(lse, lse_full[:, :, n_k - n_q:], atol=1e-12)
+
+
+def test_non_causal_rows_are_independent_of_query_count():
+    q = rnd((1, 2, 50, 64), 37)
+    k = rnd((1, 2, 20, 64), 38)
+    v = rnd((1, 2, 20, 64), 39)
+    whole = ref.attention_reference(q, k, v, return_f32=True)
+    one = ref.attention_reference(q[:, :, 7:8], k, v, return_f32=True)
+    np.testing.assert_allclose(one, whole[:, :, 7:8], atol=1e-6)
+    # against the square oracle: the first 20 query rows with 20 keys
+    sq = ref.attention_reference(q[:, :, :20], k, v, return_f32=True)
+    np.testing.assert_allclose(whole[:, :, :20], sq, atol=1e-6)
+
+
+@pytest.mark.parametrize("n_q,n_k,causal", [(1, 40, False), (7, 40, False), (7, 40, True),
+                                            (40, 7, True), (40, 7, False)])
+def test_matches_torch_sdpa_cpu(n_q, n_k, causal):
+    import torch
+    q = rnd((2, 4, n_q, 64), 40)
+    k = rnd((2, 2, n_k, 64), 41)
+    v = rnd((2, 2, n_k, 64), 42)
+    got = ref.attention_reference(q, k, v, causal=causal, return_f32=True)
+    ke, ve = ref.expand_kv_for_gqa(q, k, v)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q).float(), torch.from_numpy(ke).float(),
+        torch.from_numpy(ve).float(), is_causal=causal).numpy()
+    np.testing.assert_allclose(got, want, atol=2e-6)
+    np.testing.assert_allclose(ref.attention_f64(q, k, v, causal=causal), got, atol=2e-5)
+    chunk = ref.attention_reference_chunked(q, k, v, causal=causal, rows=3, return_f32=True)
+    np.testing.assert_allclose(chunk, got, atol=1e-6)
+
+
+def test_rows_without_visible_keys_are_zero():
+    # bottom-right with more queries than keys: query i sees keys j <= i - 30
+    q = rnd((1, 1, 40, 64), 43)
+    k = rnd((1, 1, 10, 64), 44)
+    v = rnd((1, 1, 10, 64), 45)
+    o = ref.attention_reference(q, k, v, causal=2, return_f32=True)
+    assert np.all(o[:, :, :30] == 0)
+    lse = ref.attention_lse(q, k, causal=2)
+    assert np.all(np.isneginf(lse[:, :, :30])) and np.all(np.isfinite(lse[:, :, 30:]))
+    # row 30 sees key 0 only
+    np.testing.assert_allclose(o[0, 0, 30], v[0, 0, 0].astype(np.float32), atol=0)
+    np.testing.assert_allclose(ref.attention_f64(q, k, v, causal=2)[0, 0, :30], 0)

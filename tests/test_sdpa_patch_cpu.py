@@ -1,0 +1,81 @@
+"""SDPA monkey-patch host logic (no GPU): install/remove, pass-through of
+every call the kernel cannot take, and statistics, mirroring reference
+examples/llama_attention_replacement.py:18-119."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from flash_attention_sm75 import sdpa_patch as sp
+
+
+@pytest.fixture
+def patched():
+    sp.apply_patch()
+    sp.reset_stats()
+    try:
+        yield
+    finally:
+        sp.remove_patch()
+
+
+def test_apply_and_remove_swap_the_function():
+    orig = F.scaled_dot_product_attention
+    assert orig is sp._original_sdpa
+    sp.apply_patch()
+    try:
+        assert F.scaled_dot_product_attention is sp._patched_sdpa
+        assert torch.nn.functional.scaled_dot_product_attention is sp._patched_sdpa
+        sp.apply_patch()  # idempotent
+        assert sp.patch_stats()["active"] is True
+    finally:
+        sp.remove_patch()
+    assert F.scaled_dot_product_attention is orig
+    assert sp.patch_stats()["active"] is False
+
+
+def test_reference_module_name_reexports():
+    import llama_attention_replacement as lar
+    assert lar.apply_patch is sp.apply_patch and lar._stats is sp._stats
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(is_causal=True), dict(scale=0.3),
+                                dict(attn_mask=torch.zeros(5, 7))])
+def test_cpu_calls_pass_through_unchanged(patched, kw):
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(2, 4, 5, 64, generator=g)
+    k = torch.randn(2, 4, 7, 64, generator=g)
+    v = torch.randn(2, 4, 7, 64, generator=g)
+    got = F.scaled_dot_product_attention(q, k, v, **kw)
+    want = sp._original_sdpa(q, k, v, **kw)
+    assert torch.equal(got, want)
+    s = sp.patch_stats()
+    assert (s["total"], s["flash"], s["fallback"]) == (1, 0, 1)
+    assert s["fallback_reasons"] == {"not_cuda": 1}
+
+
+def test_fallback_keeps_extra_kwargs(patched):
+    q = torch.randn(1, 4, 3, 64)
+    k = torch.randn(1, 2, 3, 64)
+    v = torch.randn(1, 2, 3, 64)
+    got = F.scaled_dot_product_attention(q, k, v, enable_gqa=True)
+    assert torch.equal(got, sp._original_sdpa(q, k, v, enable_gqa=True))
+
+
+def test_tiny_qwen2_on_cpu_is_unchanged(patched):
+    """A random-init Qwen2 (no weights are downloadable here): every attention
+    call of the CPU model falls back, so the logits are bit-identical."""
+    transformers = pytest.importorskip("transformers")
+    cfg = transformers.Qwen2Config(
+        vocab_size=500, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+        num_attention_heads=2, num_key_value_heads=1, max_position_embeddings=512,
+        attn_implementation="sdpa")
+    torch.manual_seed(0)
+    model = transformers.Qwen2ForCausalLM(cfg).eval()
+    ids = torch.randint(0, 500, (1, 20))
+    with torch.no_grad():
+        patched_logits = model(input_ids=ids).logits
+        sp.remove_patch()
+        plain = model(input_ids=ids).logits
+        sp.apply_patch()
+    assert torch.equal(patched_logits, plain)
+    assert sp._stats["fallback_reasons"].get("not_cuda") == 2
