@@ -1,7 +1,7 @@
 """Benchmark of the fused attention forward on one MI355X.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
-                  [--no-cpu-baseline] [--all]
+                  [--no-cpu-baseline] [--all] [--decode] [--hf]
 
 A step is one fused forward over one batch of synthetic input (the hot path:
 flash_attention_sm75.flash_attention_forward -> flash_attn_sm75_cuda ->
@@ -152,6 +152,98 @@ def cpu_baseline(cfg, budget_s=20.0):
     }
 
 
+# Split-K (decode) workloads: name -> (B, Hq, Hkv, Nq, Nk, D).  HBM-bound: the
+# algorithmic bytes are K + V read once plus Q read and O written.
+DECODE_CONFIGS = {
+    "D1": (32, 32, 8, 1, 8192, 128),     # batched Llama-style decode step
+    "D2": (1, 32, 8, 1, 131072, 128),    # one long-context sequence
+    "D3": (16, 14, 2, 1, 32768, 64),     # Qwen2-0.5B head layout
+}
+
+
+def time_decode(name, steps=20, warmup=5, policy=0):
+    """Median time of one flash_attention_forward_ex call (split-K kernel and
+    the combine kernel) and its HBM throughput."""
+    import torch
+
+    import flash_attn_sm75_cuda as _C
+    from flash_attention_sm75 import flash_attention_forward_ex
+
+    B, Hq, Hkv, Nq, Nk, D = DECODE_CONFIGS[name]
+    dev = torch.device("cuda", 0)
+    g = torch.Generator("cpu").manual_seed(7)
+    q = torch.randn(B, Hq, Nq, D, generator=g).half().to(dev)
+    k = torch.randn(B, Hkv, Nk, D, generator=g).half().to(dev)
+    v = torch.randn(B, Hkv, Nk, D, generator=g).half().to(dev)
+    _C.set_kernel_policy(policy)
+    try:
+        for _ in range(warmup):
+            flash_attention_forward_ex(q, k, v)
+        stream = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        torch.cuda.synchronize()
+        for i in range(steps):
+            ev[i][0].record(stream)
+            flash_attention_forward_ex(q, k, v)
+            ev[i][1].record(stream)
+        torch.cuda.synchronize()
+    finally:
+        _C.set_kernel_policy(0)
+    ms = sorted(a.elapsed_time(b) for a, b in ev)[steps // 2]
+    nbytes = 2 * B * Hkv * Nk * D * 2 + 2 * B * Hq * Nq * D * 2
+    return ms, nbytes / (ms * 1e-3) / 1e9
+
+
+def time_hf(prompt_len=4096, decode_steps=32):
+    """Random-init Qwen2-0.5B-shaped model (no weights can be downloaded):
+    prefill and teacher-forced KV-cache decode, unpatched vs patched SDPA."""
+    import torch
+    import transformers
+
+    from flash_attention_sm75 import sdpa_patch
+
+    cfg = transformers.Qwen2Config(
+        vocab_size=151936, hidden_size=896, intermediate_size=4864, num_hidden_layers=24,
+        num_attention_heads=14, num_key_value_heads=2, max_position_embeddings=32768,
+        attn_implementation="sdpa")
+    torch.manual_seed(0)
+    model = transformers.Qwen2ForCausalLM(cfg).half().to("cuda").eval()
+    g = torch.Generator("cpu").manual_seed(1)
+    ids = torch.randint(0, cfg.vocab_size, (1, prompt_len + decode_steps), generator=g).cuda()
+
+    def run():
+        with torch.no_grad():
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = model(input_ids=ids[:, :prompt_len], use_cache=True)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            cache = out.past_key_values
+            for t in range(decode_steps):
+                out = model(input_ids=ids[:, prompt_len + t:prompt_len + t + 1],
+                            past_key_values=cache, use_cache=True)
+                cache = out.past_key_values
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+        return t1 - t0, (t2 - t1) / decode_steps
+
+    res = {}
+    for label in ("unpatched", "patched"):
+        if label == "patched":
+            sdpa_patch.apply_patch()
+            sdpa_patch.reset_stats()
+        try:
+            run()  # warm-up
+            res[label] = min(run() for _ in range(3))
+            if label == "patched":
+                res["stats"] = sdpa_patch.patch_stats()
+        finally:
+            if label == "patched":
+                sdpa_patch.remove_patch()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,6 +253,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--all", action="store_true", help="also time C1..C5 (stderr)")
+    ap.add_argument("--decode", action="store_true",
+                    help="also time the split-K decode workloads D1..D3 (stderr)")
+    ap.add_argument("--hf", action="store_true",
+                    help="also time a random-init Qwen2-0.5B-shaped model, unpatched vs "
+                         "patched SDPA (stderr)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise copy of 256 MiB (known HBM bytes) "
                          "to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
@@ -194,6 +291,21 @@ def main():
             med = km[len(km) // 2]
             log(f"[{c}] {DESCR[c]}: median kernel {med:.4f} ms -> "
                 f"{flops(b_, hq_, n_, d_, ca_) / med / 1e9:.1f} TFLOPS")
+
+    if args.decode:
+        for c in sorted(DECODE_CONFIGS):
+            ms, gbs = time_decode(c)
+            ms_pre, gbs_pre = time_decode(c, steps=5, warmup=2, policy=1)
+            log(f"[{c}] decode B,Hq,Hkv,Nq,Nk,D={DECODE_CONFIGS[c]}: split-K {ms:.4f} ms -> "
+                f"{gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM peak); "
+                f"128-row prefill kernel {ms_pre:.4f} ms ({gbs_pre:.0f} GB/s)")
+
+    if args.hf:
+        r = time_hf()
+        (pu, du), (pp, dp) = r["unpatched"], r["patched"]
+        log(f"[hf] Qwen2-0.5B shape, random init, prompt 4096: prefill {pu * 1e3:.1f} ms -> "
+            f"{pp * 1e3:.1f} ms patched; decode {du * 1e3:.2f} -> {dp * 1e3:.2f} ms/token; "
+            f"patch stats {r['stats']}")
 
     wall, kern_ms = time_gpu(cfg, args.steps, args.warmup)
     ms_per_step = wall * 1e3 / args.steps

@@ -81,13 +81,28 @@ void check_fused_shapes(const torch::Tensor& Q, const torch::Tensor& K,
               "flash_attention_forward supports head_dim=64 or 128, got ", head_dim);
 }
 
+// Runs fa_sm75_forward with a workspace from torch's caching allocator when
+// the call can use one (the split-K path).  The workspace is released when
+// this returns; the allocator only hands it out again to work ordered after
+// the launch on the same stream.
+void forward_with_workspace(fa_fwd_params& p, const torch::Tensor& Q, const char* tag) {
+  p.stream = c10::hip::getCurrentHIPStream(Q.device().index()).stream();
+  const int64_t ws = fa_sm75_workspace_size(&p);
+  torch::Tensor work;
+  if (ws > 0) {
+    work = torch::empty({ws}, Q.options().dtype(torch::kUInt8));
+    p.workspace = work.data_ptr();
+    p.workspace_bytes = ws;
+  }
+  const int st = fa_sm75_forward(&p);
+  TORCH_CHECK(st == FA_OK, tag, ": ", fa_sm75_last_error());
+}
+
 void run_fused(const torch::Tensor& Q, const torch::Tensor& K, const torch::Tensor& V,
                torch::Tensor& O, float* lse, bool causal, float scale) {
   const at::OptionalDeviceGuard guard(at::device_of(Q));
   fa_fwd_params p = make_params(Q, K, V, O, lse, causal, scale);
-  p.stream = c10::hip::getCurrentHIPStream(Q.device().index()).stream();
-  const int st = fa_sm75_forward(&p);
-  TORCH_CHECK(st == FA_OK, "flash_attention_forward: ", fa_sm75_last_error());
+  forward_with_workspace(p, Q, "flash_attention_forward");
 }
 
 torch::Tensor flash_attention_forward(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
@@ -184,9 +199,7 @@ std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_
   p.o_stride_n = on; p.o_stride_h = eff_stride(O, 1, 0); p.o_stride_b = eff_stride(O, 0, 0);
   p.scale = (float)scale;
   p.causal = (int)causal;
-  p.stream = c10::hip::getCurrentHIPStream(Q.device().index()).stream();
-  const int st = fa_sm75_forward(&p);
-  TORCH_CHECK(st == FA_OK, "flash_attention_forward_ex: ", fa_sm75_last_error());
+  forward_with_workspace(p, Q, "flash_attention_forward_ex");
   return {O, L};
 }
 
@@ -251,4 +264,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("Q"), pybind11::arg("K"), pybind11::arg("V"), pybind11::arg("causal"),
         pybind11::arg("scale"), pybind11::arg("return_lse") = false);
   m.def("abi_version", []() { return fa_sm75_abi_version(); });
+  m.def("set_kernel_policy", [](int policy) {
+    TORCH_CHECK(fa_sm75_set_kernel_policy(policy) == FA_OK,
+                "kernel policy must be 0 (auto), 1 (narrow) or 2 (wide), got ", policy);
+  });
+  m.def("get_kernel_policy", []() { return fa_sm75_get_kernel_policy(); });
 }

@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <atomic>
 #include <cstring>
+#include <string>
 
 #include "fa_internal.h"
 #include "flash_attn_sm75.h"
@@ -76,6 +77,10 @@ int validate(const fa_fwd_params* p, bool fused) {
     return fail(FA_ERR_INVALID_ARGUMENT, "Q, K, V and O pointers must not be NULL");
   if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o))
     return fail(FA_ERR_MISALIGNED, "Q, K, V and O must be 16-byte aligned");
+  if (p->workspace != nullptr && !aligned16(p->workspace))
+    return fail(FA_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+  if (p->workspace_bytes < 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "workspace_bytes must be non-negative");
   const int64_t strides[12] = {p->q_stride_b, p->q_stride_h, p->q_stride_n,
                                p->k_stride_b, p->k_stride_h, p->k_stride_n,
                                p->v_stride_b, p->v_stride_h, p->v_stride_n,
@@ -94,9 +99,10 @@ int validate(const fa_fwd_params* p, bool fused) {
   if (p->seq_len > INT32_MAX / 2 || nk > INT32_MAX / 2)
     return fail(FA_ERR_TOO_LARGE, "seq_len %lld / seq_len_kv %lld exceeds the supported maximum",
                 (long long)p->seq_len, (long long)nk);
-  // K/V tiles are read through 32-bit buffer windows over one (batch, head).
-  if (nk * p->k_stride_n * 2 > (int64_t)INT32_MAX ||
-      nk * p->v_stride_n * 2 > (int64_t)INT32_MAX)
+  // K/V tiles are read through 32-bit buffer windows over one (batch, head),
+  // with offsets up to one tile past the last key.
+  if ((nk + 64) * p->k_stride_n * 2 > (int64_t)INT32_MAX ||
+      (nk + 64) * p->v_stride_n * 2 > (int64_t)INT32_MAX)
     return fail(FA_ERR_TOO_LARGE, "seq_len_kv * row stride of K/V exceeds 2^31 bytes");
   // One 1-D grid of batch*heads_q*ceil(seq_len/128) workgroups of 256
   // threads; the thread count must stay below 2^32.
@@ -189,10 +195,31 @@ int fa_sm75_forward(const fa_fwd_params* p) {
   if (st != FA_OK) return st;
   if (p->batch == 0 || p->heads_q == 0 || p->seq_len == 0) return FA_OK;
   const fa::FwdArgs a = make_args(p);
-  fa::launch_fused_forward(a, (int)p->batch, (int)p->head_dim, p->causal != 0,
-                           g_kernel_policy.load(std::memory_order_relaxed),
-                           reinterpret_cast<hipStream_t>(p->stream));
+  const int policy = g_kernel_policy.load(std::memory_order_relaxed);
+  const hipStream_t stream = reinterpret_cast<hipStream_t>(p->stream);
+  if (policy == FA_POLICY_AUTO && fa::decode_eligible(a)) {
+    const int64_t room = p->workspace != nullptr ? p->workspace_bytes : 0;
+    const fa::DecodePlan plan =
+        fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, room);
+    fa::launch_decode_forward(a, plan, (int)p->head_dim, p->causal != 0, p->workspace, stream);
+  } else {
+    fa::launch_fused_forward(a, (int)p->batch, (int)p->head_dim, p->causal != 0, policy,
+                             stream);
+  }
   return check_launch();
+}
+
+int64_t fa_sm75_workspace_size(const fa_fwd_params* p) {
+  const std::string saved = g_last_error;
+  const int st = validate(p, true);
+  std::snprintf(g_last_error, sizeof(g_last_error), "%s", saved.c_str());
+  if (st != FA_OK || p->batch == 0 || p->heads_q == 0 || p->seq_len == 0) return 0;
+  const fa::FwdArgs a = make_args(p);
+  if (g_kernel_policy.load(std::memory_order_relaxed) != FA_POLICY_AUTO ||
+      !fa::decode_eligible(a))
+    return 0;
+  return fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, INT64_MAX)
+      .workspace_bytes;
 }
 
 int fa_sm75_set_kernel_policy(int policy) {

@@ -1,0 +1,431 @@
+// Split-K forward for few query rows per K/V head (KV-cache decode).
+//
+// When heads_q / heads_kv * seq_len <= 32, all query rows that read one
+// (batch, KV head) -- the "unit" -- fit the 32 query columns of one MFMA
+// tile, and the work is streaming K and V once from HBM: the path is
+// HBM-bound (2 * Nk * D * 2 bytes per unit against 4 * rows * Nk * D FLOP).
+// The 128-row prefill kernel would read K/V once per query head and leave
+// most of its rows empty, so this path reorganises the work:
+//
+//   * grid = units x splits: split s of a unit takes key tiles
+//     [s * chunk, (s + 1) * chunk) of 32 keys; the four waves of a workgroup
+//     take every fourth tile of the chunk and run independently (no
+//     workgroup barrier inside the loop): K straight from HBM into VGPRs as
+//     the MFMA A operand, V through a per-wave, double-buffered LDS tile
+//     (direct-to-LDS loads, read back transposed with ds_read_b64_tr_b16);
+//   * the four waves' (max, sum, O) merge through LDS at the end;
+//   * with one split the workgroup writes O (and LSE) directly; otherwise it
+//     writes an fp32 partial (unnormalised O, running max in log2 units, sum)
+//     to the caller's workspace and fa_decode_combine merges the splits.
+//
+// The MFMA formulation, the LDS tile layout, the online-softmax numerics and
+// the lazy rescale are those of the prefill kernel (fa_fwd.hip): S^T = K Q^T
+// with one query per lane, P kept in registers as the B operand of
+// O^T = V^T P^T.  Query column r of unit (b, hkv) is query head
+// hkv * group + r / Nq, query index r % Nq.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "fa_internal.h"
+
+#include "fa_kernel_common.h"
+
+namespace fa {
+namespace {
+
+constexpr int kDecTile = 32;       // keys per wave tile
+constexpr int kDecMinTiles = 8;    // fewest tiles a split is given
+constexpr int kDecTargetWgs = 512; // two workgroups per CU
+
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+template <int D>
+struct DecLds {
+  static constexpr int Pitch = D + 32;                 // same padded rows as Lds<D>
+  static constexpr int Tile = kDecTile * Pitch;        // halves per V tile
+  static constexpr int Segs = Tile * 2 / 1024;         // 1 KB direct-load segments
+  static_assert(Tile * 2 % 1024 == 0, "V tile must be whole segments");
+};
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
+// vmcnt[5:4] at bits 15:14, expcnt 7, lgkmcnt 15), followed by a compiler
+// memory barrier: the waitcnt intrinsic does not touch memory as far as the
+// compiler knows, so without it the LDS reads that depend on the wait could
+// be hoisted above it.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+template <int D, bool CAUSAL>
+__global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d) {
+  const FwdArgs& a = d.f;
+  using L = DecLds<D>;
+  constexpr int KK = D / 16;   // 16-wide contraction steps of S^T
+  constexpr int MT = D / 32;   // 32-row output tiles of O^T
+  constexpr int NPV = 2 * MT;  // P V MFMAs per 32-key tile
+  constexpr int SEGS = L::Segs;
+
+  // Per-wave V tiles: wave w uses [w * Tile, (w + 1) * Tile) of each array.
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds0[kWaves * L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds1[kWaves * L::Tile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // Wave-uniform (in a scalar register): the per-wave buffer windows and LDS
+  // destinations derived from it must be scalar, or every direct load would
+  // become a loop over the distinct values of the wave.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hi = lane >> 5;
+  const int ql = lane & 31;
+  const int grp = lane >> 4;
+  const int gi = lane & 15;
+
+  const int unit = (int)blockIdx.x / d.splits;
+  const int split = (int)blockIdx.x - unit * d.splits;
+  const int hkv_count = a.hq / a.group;
+  const int b = unit / hkv_count;
+  const int hkv = unit - b * hkv_count;
+  const int nq = a.n;
+  const int NK = a.nk;
+
+  // This lane's query column.
+  const bool row_ok = ql < d.rows;
+  const int g = ql / nq;
+  const int qi = ql - g * nq;
+  const int hq = hkv * a.group + g;
+
+  half8 qf[KK];
+  if (row_ok) {
+    const _Float16* qp = a.q + b * a.qsb + hq * a.qsh + (int64_t)qi * a.qsn + 8 * hi;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qf[kk] = *(const half8*)(qp + 16 * kk);
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qf[kk] = (half8)(_Float16)0;
+  }
+  if (a.negate_q) {
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qf[kk] = -qf[kk];
+  }
+
+  // Tiles of this split, and this wave's share (every fourth one).
+  const int t_begin = split * d.chunk_tiles;
+  const int t_end = min(t_begin + d.chunk_tiles, d.tiles);
+  const int nt_w = t_end - t_begin > wave ? (t_end - t_begin - wave + kWaves - 1) / kWaves : 0;
+  const int key0 = t_begin * kDecTile;
+  const _Float16* Kp = a.k + b * a.ksb + hkv * a.ksh;
+  const _Float16* Vp = a.v + b * a.vsb + hkv * a.vsh;
+
+  // Loads of tile it are issued whether or not the tile exists (`valid`);
+  // a missing tile reads through an empty window (zeros, no memory traffic),
+  // so every iteration has the same loads in flight and one vmcnt value
+  // serves all of them (a conditional load would make the compiler wait
+  // for the worst case and serialise the prefetch).
+  // K operand of tile it: key row (tile key base + ql), dims 16 kk + 8 hi;
+  // rows past the last key read as zeros.
+  const int k_rows_left = NK - key0;
+  const int k_bytes = k_rows_left > 0 ? k_rows_left * (int)a.ksn * 2 : 0;
+  auto load_k = [&](int it, half8 (&kf)[KK], bool valid) {
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kp + (int64_t)key0 * a.ksn, valid ? k_bytes : 0);
+    const int key = (wave + kWaves * it) * kDecTile + ql;
+    const int voff = key * (int)a.ksn * 2 + 16 * hi;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      kf[kk] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, voff + 32 * kk, 0, 0));
+  };
+
+  // V direct loads: segment s, lane l covers tile bytes [1024 s + 16 l, +16).
+  int goff_v[SEGS];
+#pragma unroll
+  for (int s = 0; s < SEGS; ++s) {
+    const int pos = s * 1024 + 16 * lane;
+    const int row = pos / (2 * L::Pitch);
+    const int within = pos - row * (2 * L::Pitch);
+    if (within < 2 * D) {
+      const int c = (within >> 4) ^ ((row >> 2) & 3);
+      goff_v[s] = (int)(row * a.vsn * 2) + 16 * c;
+    } else {
+      goff_v[s] = -16;  // padding: past any window -> zeros
+    }
+  }
+  auto load_v = [&](int it, _Float16* tile, bool valid) {
+    const int kb = key0 + (wave + kWaves * it) * kDecTile;
+    const int rows_left = valid ? NK - kb : 0;
+    const __amdgpu_buffer_rsrc_t rv =
+        make_rsrc(Vp + (int64_t)kb * a.vsn, rows_left > 0 ? rows_left * (int)a.vsn * 2 : 0);
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) direct_load16(rv, (lds_void*)(tile + s * 512), goff_v[s]);
+  };
+  _Float16* const my_v0 = v_lds0 + wave * L::Tile;
+  _Float16* const my_v1 = v_lds1 + wave * L::Tile;
+
+  const int v_row = 4 * hi + (gi >> 2);
+  const int v_c = 2 * (grp & 1) + ((gi & 3) >> 1);
+  const int v_base0 = v_row * L::Pitch + 8 * (v_c ^ hi) + 4 * (gi & 1);
+  const int v_base1 = (v_row + 8) * L::Pitch + 8 * (v_c ^ (hi + 2)) + 4 * (gi & 1);
+  auto read_v = [&](const _Float16* Vs, int v) -> half8 {
+    const int ks = v / MT, mt = v % MT;
+    const int imm = 16 * ks * L::Pitch + 32 * mt;
+    const half4 lo = ds_read_tr16(Vs + v_base0 + imm);
+    const half4 hi4 = ds_read_tr16(Vs + v_base1 + imm);
+    return __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+
+  float16v oacc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) oacc[mt] = (float16v)0.0f;
+  float m_run = -__builtin_inff();
+  float l_run = 0.0f;
+  const float c2 = a.c;
+  const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+  const int diag_row = qi + a.diag;  // causal: keys <= diag_row are visible
+
+  half8 kA[KK], kB[KK];
+
+  // One tile: S, softmax, P V.  The loads of the next tile are issued first.
+  auto step = [&](int it, half8 (&kc)[KK], half8 (&kn)[KK], _Float16* vc, _Float16* vn) {
+    const bool has_next = it + 1 < nt_w;
+    load_k(it + 1, kn, has_next);
+    load_v(it + 1, vn, has_next);
+    float16v s = (float16v)0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kc[kk], qf[kk], s, 0, 0, 0);
+
+    const int kstart = key0 + (wave + kWaves * it) * kDecTile;
+    const bool need_mask =
+        (kstart + kDecTile > NK) || (CAUSAL && kstart + kDecTile - 1 > a.diag);
+    if (need_mask) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kstart + 8 * (i >> 2) + 4 * hi + (i & 3);
+        if (key >= NK || (CAUSAL && key > diag_row)) s[i] = -__builtin_inff();
+      }
+    }
+    float mx = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    mx = halves_max(mx);
+    const bool grow = (mx - m_run) * c2 > kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
+      const float alpha =
+          (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) oacc[mt] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = ((m_run == -__builtin_inff()) ? 0.0f : m_run) * c2;
+    half8 pf[2];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c2, -mc));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i + 1], c2, -mc));
+      const half2v pr = {(_Float16)p0, (_Float16)p1};
+      pf[i >> 3][i & 7] = pr[0];
+      pf[i >> 3][(i & 7) + 1] = pr[1];
+      l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
+    }
+    // V of this tile has landed once only the next tile's loads are pending
+    // (loads complete in order).
+    wait_vmcnt<KK + SEGS>();
+    half8 vf[NPV];
+#pragma unroll
+    for (int v = 0; v < NPV; ++v) vf[v] = read_v(vc, v);
+#pragma unroll
+    for (int v = 0; v < NPV; ++v) {
+      const int ks = v / MT, mt = v % MT;
+      oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[v], pf[ks], oacc[mt], 0, 0, 0);
+    }
+  };
+
+  if (nt_w > 0) {
+    load_k(0, kA, true);
+    load_v(0, my_v0, true);
+    int it = 0;
+    for (; it + 1 < nt_w; it += 2) {
+      step(it, kA, kB, my_v0, my_v1);
+      step(it + 1, kB, kA, my_v1, my_v0);
+    }
+    if (it < nt_w) step(it, kA, kB, my_v0, my_v1);
+  }
+
+  // ---- merge the four waves through LDS (the V tiles are free now) --------
+  const float l_tot = halves_sum(l_run);
+  __syncthreads();
+  {
+    float* o_lo = (float*)(v_lds0 + wave * L::Tile);
+    float* o_hi = (float*)(v_lds1 + wave * L::Tile);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float* dst = (mt < MT / 2 ? o_lo : o_hi) + (mt % (MT / 2)) * 16 * 64;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dst[i * 64 + lane] = oacc[mt][i];
+    }
+    float* ml = o_lo + (MT / 2) * 16 * 64;
+    ml[lane] = m_run;
+    ml[64 + lane] = l_tot;
+  }
+  __syncthreads();
+  if (wave >= MT) return;
+  const int mt = wave;  // this wave merges output tile mt
+  float m_w[kWaves], M = -__builtin_inff();
+#pragma unroll
+  for (int u = 0; u < kWaves; ++u) {
+    const float* ml = (const float*)(v_lds0 + u * L::Tile) + (MT / 2) * 16 * 64;
+    m_w[u] = ml[lane];
+    M = fmaxf(M, m_w[u]);
+  }
+  float Ltot = 0.0f;
+  float o[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kWaves; ++u) {
+    const float f = (m_w[u] == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_w[u] - M) * c2);
+    const float* base = (const float*)((mt < MT / 2 ? v_lds0 : v_lds1) + u * L::Tile) +
+                        (mt % (MT / 2)) * 16 * 64;
+    const float* ml = (const float*)(v_lds0 + u * L::Tile) + (MT / 2) * 16 * 64;
+    Ltot += f * ml[64 + lane];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] += f * base[i * 64 + lane];
+  }
+  if (!row_ok) return;
+  if (d.splits == 1) {
+    const float inv = (Ltot > 0.0f) ? (1.0f / Ltot) : 0.0f;
+    _Float16* op = a.o + b * a.osb + hq * a.osh + (int64_t)qi * a.osn + 32 * mt + 4 * hi;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      half4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (_Float16)(o[4 * g4 + e] * inv);
+      *(half4*)(op + 8 * g4) = v;
+    }
+    if (a.lse != nullptr && mt == 0 && hi == 0) {
+      const float m_use = (M == -__builtin_inff()) ? 0.0f : M;
+      a.lse[((int64_t)b * a.hq + hq) * nq + qi] =
+          (m_use * c2 + __builtin_log2f(Ltot)) * 0.69314718055994530942f;
+    }
+  } else {
+    const int64_t p = ((int64_t)unit * d.splits + split) * d.rows + ql;
+    float* po = d.part_o + p * D + 32 * mt + 4 * hi;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      float4 v = {o[4 * g4], o[4 * g4 + 1], o[4 * g4 + 2], o[4 * g4 + 3]};
+      *(float4*)(po + 8 * g4) = v;
+    }
+    if (mt == 0 && hi == 0) {
+      d.part_ml[2 * p] = (M == -__builtin_inff()) ? -__builtin_inff() : M * c2;
+      d.part_ml[2 * p + 1] = Ltot;
+    }
+  }
+}
+
+// Merges the splits of one (unit, query column): one wave, D / 64 dims per
+// lane.  O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, M = max_s m_s.
+template <int D>
+__global__ void __launch_bounds__(64) fa_decode_combine(const DecArgs d) {
+  const FwdArgs& a = d.f;
+  constexpr int PER = D / 64;
+  const int lane = threadIdx.x;
+  const int unit = (int)blockIdx.x / d.rows;
+  const int r = (int)blockIdx.x - unit * d.rows;
+  const int hkv_count = a.hq / a.group;
+  const int b = unit / hkv_count;
+  const int hkv = unit - b * hkv_count;
+  const int g = r / a.n;
+  const int qi = r - g * a.n;
+  const int hq = hkv * a.group + g;
+  const int64_t p0 = (int64_t)unit * d.splits * d.rows + r;  // split s: p0 + s * rows
+
+  float M = -__builtin_inff();
+  for (int s = 0; s < d.splits; ++s) M = fmaxf(M, d.part_ml[2 * (p0 + (int64_t)s * d.rows)]);
+  float Ltot = 0.0f;
+  float o[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) o[e] = 0.0f;
+  for (int s = 0; s < d.splits; ++s) {
+    const int64_t p = p0 + (int64_t)s * d.rows;
+    const float ms = d.part_ml[2 * p];
+    const float f = (ms == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+    Ltot += f * d.part_ml[2 * p + 1];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) o[e] += f * d.part_o[p * D + lane + 64 * e];
+  }
+  const float inv = (Ltot > 0.0f) ? (1.0f / Ltot) : 0.0f;
+  _Float16* op = a.o + b * a.osb + hq * a.osh + (int64_t)qi * a.osn;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) op[lane + 64 * e] = (_Float16)(o[e] * inv);
+  if (a.lse != nullptr && lane == 0) {
+    const float m_use = (M == -__builtin_inff()) ? 0.0f : M;
+    a.lse[((int64_t)b * a.hq + hq) * a.n + qi] =
+        (m_use + __builtin_log2f(Ltot)) * 0.69314718055994530942f;
+  }
+}
+
+}  // namespace
+
+bool decode_eligible(const FwdArgs& a) { return (int64_t)a.group * a.n <= kDecodeMaxRows; }
+
+DecodePlan plan_decode(const FwdArgs& a, int batch, int head_dim, bool causal,
+                       int64_t workspace_bytes) {
+  DecodePlan pl;
+  pl.rows = a.group * a.n;
+  pl.units = batch * (a.hq / a.group);
+  // Keys any query row can see.
+  int64_t nk_eff = a.nk;
+  if (causal) nk_eff = std::min<int64_t>(a.nk, std::max<int64_t>(0, (int64_t)a.n + a.diag));
+  pl.tiles = (int)((nk_eff + kDecTile - 1) / kDecTile);
+  int splits = (kDecTargetWgs + pl.units - 1) / pl.units;
+  splits = std::min(splits, std::max(1, pl.tiles / kDecMinTiles));
+  splits = std::max(splits, 1);
+  pl.chunk_tiles = std::max(1, (pl.tiles + splits - 1) / splits);
+  pl.splits = std::max(1, (pl.tiles + pl.chunk_tiles - 1) / pl.chunk_tiles);
+  pl.workspace_bytes =
+      pl.splits > 1 ? (int64_t)pl.units * pl.splits * pl.rows * (head_dim + 2) * 4 : 0;
+  if (pl.workspace_bytes > workspace_bytes) {  // not enough room: one split
+    pl.splits = 1;
+    pl.chunk_tiles = std::max(1, pl.tiles);
+    pl.workspace_bytes = 0;
+  }
+  return pl;
+}
+
+int launch_decode_forward(const FwdArgs& a, const DecodePlan& pl, int head_dim, bool causal,
+                          void* workspace, hipStream_t stream) {
+  DecArgs d;
+  d.f = a;
+  d.rows = pl.rows;
+  d.splits = pl.splits;
+  d.chunk_tiles = pl.chunk_tiles;
+  d.tiles = pl.tiles;
+  d.part_o = static_cast<float*>(workspace);
+  d.part_ml = pl.splits > 1
+                  ? d.part_o + (int64_t)pl.units * pl.splits * pl.rows * head_dim
+                  : nullptr;
+  const dim3 grid((unsigned)((int64_t)pl.units * pl.splits));
+#define FA_DEC(DD, C) hipLaunchKernelGGL((fa_decode_kernel<DD, C>), grid, dim3(kThreads), 0, stream, d)
+  if (head_dim == 128) {
+    if (causal) FA_DEC(128, true); else FA_DEC(128, false);
+  } else {
+    if (causal) FA_DEC(64, true); else FA_DEC(64, false);
+  }
+#undef FA_DEC
+  if (pl.splits > 1) {
+    const dim3 cgrid((unsigned)((int64_t)pl.units * pl.rows));
+    if (head_dim == 128)
+      hipLaunchKernelGGL(fa_decode_combine<128>, cgrid, dim3(64), 0, stream, d);
+    else
+      hipLaunchKernelGGL(fa_decode_combine<64>, cgrid, dim3(64), 0, stream, d);
+  }
+  return 0;
+}
+
+}  // namespace fa

@@ -44,6 +44,29 @@ constexpr int kBlockMWide = 256;
 int launch_fused_forward_wide(const FwdArgs& a, int batch, bool causal, hipStream_t stream);
 int fused_block_m();
 
+// Split-K path for few query rows per K/V head (fa_decode.hip): taken when
+// heads_q / heads_kv * seq_len <= kDecodeMaxRows.
+constexpr int kDecodeMaxRows = 32;
+struct DecArgs {
+  FwdArgs f;
+  int rows;         // query columns per unit: group * n
+  int splits;       // key ranges per unit
+  int chunk_tiles;  // 32-key tiles per split
+  int tiles;        // 32-key tiles any row can see
+  float* part_o;    // [units, splits, rows, D] unnormalised O (splits > 1)
+  float* part_ml;   // [units, splits, rows, 2]: max (log2 units), sum
+};
+struct DecodePlan {
+  int rows, units, tiles, splits, chunk_tiles;
+  int64_t workspace_bytes;  // 0 when splits == 1
+};
+bool decode_eligible(const FwdArgs& a);
+// Splits for a workspace of `workspace_bytes` (one split if it is too small).
+DecodePlan plan_decode(const FwdArgs& a, int batch, int head_dim, bool causal,
+                       int64_t workspace_bytes);
+int launch_decode_forward(const FwdArgs& a, const DecodePlan& plan, int head_dim, bool causal,
+                          void* workspace, hipStream_t stream);
+
 // Three-kernel path through an fp32 [B*Hq, N, N] score workspace.
 int launch_naive_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
                          float scale, float* workspace, hipStream_t stream);

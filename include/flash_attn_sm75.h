@@ -80,6 +80,11 @@ typedef struct fa_fwd_params {
   int causal;        /* an fa_causal value */
   void* stream;      /* hipStream_t; NULL selects the default stream */
   int64_t seq_len_kv; /* key/value rows Nk; 0 means Nk = seq_len */
+  void* workspace;    /* optional device scratch for the split-K path (few query
+                         rows per K/V head, e.g. KV-cache decode), or NULL */
+  int64_t workspace_bytes; /* its size; fa_sm75_workspace_size() gives the
+                         amount for full parallelism.  With less, the call
+                         still runs, on fewer workgroups, and allocates nothing */
 } fa_fwd_params;
 
 /* Fills strides for contiguous [B,H,N,D] Q/O and [B,Hkv,Nk,D] K/V tensors. */
@@ -88,8 +93,15 @@ void fa_sm75_set_contiguous_strides(fa_fwd_params* p);
 /* Fused MFMA forward.  Replaces the launch in reference
  * src/kernels/flash_attention_forward.cu:795-817 (and the GQA expansion of
  * src/flash_attention_sm75/ops.py:6-27).  Asynchronous on p->stream.
+ * Calls with (heads_q / heads_kv) * seq_len <= 32 take the split-K path,
+ * which uses p->workspace when it is large enough.
  * Returns FA_OK or an fa_status; fa_sm75_last_error() holds the message. */
 int fa_sm75_forward(const fa_fwd_params* p);
+
+/* Workspace bytes fa_sm75_forward can use for this call (0: none); 0 also
+ * for invalid parameters, which fa_sm75_forward reports.  No reference
+ * counterpart (the reference has no decode path). */
+int64_t fa_sm75_workspace_size(const fa_fwd_params* p);
 
 /* Three-pass reference-style path (QK^T -> row softmax -> PV) through an fp32
  * score workspace of batch*heads_q*seq_len*seq_len floats.  Replaces reference
@@ -108,10 +120,11 @@ const char* fa_sm75_status_string(int status);
 int fa_sm75_abi_version(void);
 
 /* Fused-kernel selection, process-wide (no reference counterpart: a tuning
- * and testing control).  AUTO picks by problem size; NARROW forces 128-row
- * workgroups (two waves per SIMD); WIDE forces 256-row workgroups (one wave
- * per SIMD, 64 rows per wave; head_dim 128 only, head_dim 64 stays NARROW).
- * Both kernels compute the same function. */
+ * and testing control).  AUTO picks by problem size (the split-K path for
+ * few query rows per K/V head, else 128-row workgroups); NARROW forces
+ * 128-row workgroups (two waves per SIMD); WIDE forces 256-row workgroups
+ * (one wave per SIMD, 64 rows per wave; head_dim 128 only, head_dim 64 stays
+ * NARROW).  All kernels compute the same function. */
 enum fa_kernel_policy { FA_POLICY_AUTO = 0, FA_POLICY_NARROW = 1, FA_POLICY_WIDE = 2 };
 int fa_sm75_set_kernel_policy(int policy); /* FA_OK or FA_ERR_INVALID_ARGUMENT */
 int fa_sm75_get_kernel_policy(void);

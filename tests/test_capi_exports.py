@@ -25,7 +25,7 @@ def declared_functions():
                 continue
             # a declaration: preceded by a type, ends with ');'
             tail = text[m.end():text.find(";", m.end()) + 1]
-            if tail.endswith(");") and re.search(r"(void|int|char\s*\*|char)\s*\**$", prefix):
+            if tail.endswith(");") and re.search(r"(void|int|int64_t|char\s*\*|char)\s*\**$", prefix):
                 names.append(name)
     return sorted(set(names))
 
@@ -49,6 +49,7 @@ def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("fa_sm75_forward", "fa_sm75_naive_forward", "fa_sm75_last_error",
               "fa_sm75_status_string", "fa_sm75_abi_version", "fa_sm75_set_contiguous_strides",
+              "fa_sm75_workspace_size",
               "launch_flash_attention_forward", "launch_flash_attention_forward_scalar",
               "launch_flash_attention_forward_wmma_qk", "launch_naive_attention"):
         assert n in names, n
@@ -100,6 +101,8 @@ def test_contiguous_strides_separate_kv_length(lib):
     (dict(causal=-1), 1, b"causal must be"),
     (dict(seq_len_kv=-5), 1, b"non-negative"),
     (dict(seq_len_kv=1 << 30), 5, b"exceeds the supported maximum"),
+    (dict(workspace=0x10004, workspace_bytes=64), 4, b"workspace must be 16-byte aligned"),
+    (dict(workspace_bytes=-1), 1, b"workspace_bytes must be non-negative"),
 ])
 def test_validation_errors(lib, kw, status, msg):
     p = make(lib, **kw)
@@ -126,6 +129,32 @@ def test_naive_validation(lib):
     p3 = make(lib, seq_len_kv=65)
     assert lib.fa_sm75_naive_forward(ctypes.byref(p3), ctypes.c_void_p(0x10000)) == 1
     assert b"seq_len_kv == seq_len" in lib.fa_sm75_last_error()
+
+
+def test_workspace_size(lib):
+    lib.fa_sm75_workspace_size.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_workspace_size.restype = ctypes.c_int64
+    # prefill-sized call: the 128-row kernel needs no workspace
+    p = make(lib)
+    assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == 0
+    # decode: 4 query heads over 2 KV heads, one query row, 8192 keys
+    p = make(lib, seq_len=1, seq_len_kv=8192)
+    lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+    ws = lib.fa_sm75_workspace_size(ctypes.byref(p))
+    rows, units, d = 2, 2, 128
+    assert ws > 0 and ws % (units * rows * (d + 2) * 4) == 0
+    # invalid parameters: 0, and the last error is left alone
+    lib.fa_sm75_forward(ctypes.byref(make(lib, head_dim=96)))
+    msg = lib.fa_sm75_last_error()
+    assert lib.fa_sm75_workspace_size(ctypes.byref(make(lib, head_dim=48, seq_len=1))) == 0
+    assert lib.fa_sm75_last_error() == msg
+    # a forced kernel policy never takes the split-K path
+    lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
+    try:
+        lib.fa_sm75_set_kernel_policy(1)
+        assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == 0
+    finally:
+        lib.fa_sm75_set_kernel_policy(0)
 
 
 def test_abi_version(lib):
