@@ -328,13 +328,23 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   }
 }
 
-// Merges the splits of one (unit, query column): one wave, D / 64 dims per
-// lane.  O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, M = max_s m_s.
+// Merges the splits of one (unit, query column) with 256 threads:
+// O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, M = max_s m_s.
+// The split weights are computed once (one thread per split) and kept in
+// LDS; the O sum is spread over 256 / D groups of D threads (one dimension
+// each), each taking every (256 / D)-th split with independent loads in
+// flight, and the groups' sums meet in LDS.
+constexpr int kCombineThreads = 256;
+constexpr int kMaxSplits = 1024;
+
 template <int D>
-__global__ void __launch_bounds__(64) fa_decode_combine(const DecArgs d) {
+__global__ void __launch_bounds__(kCombineThreads) fa_decode_combine(const DecArgs d) {
   const FwdArgs& a = d.f;
-  constexpr int PER = D / 64;
-  const int lane = threadIdx.x;
+  constexpr int GROUPS = kCombineThreads / D;
+  __shared__ float w_s[kMaxSplits];
+  __shared__ float red[kCombineThreads];
+  __shared__ float o_part[GROUPS][D];
+  const int tid = threadIdx.x;
   const int unit = (int)blockIdx.x / d.rows;
   const int r = (int)blockIdx.x - unit * d.rows;
   const int hkv_count = a.hq / a.group;
@@ -344,26 +354,61 @@ __global__ void __launch_bounds__(64) fa_decode_combine(const DecArgs d) {
   const int qi = r - g * a.n;
   const int hq = hkv * a.group + g;
   const int64_t p0 = (int64_t)unit * d.splits * d.rows + r;  // split s: p0 + s * rows
+  const int S = d.splits;
 
-  float M = -__builtin_inff();
-  for (int s = 0; s < d.splits; ++s) M = fmaxf(M, d.part_ml[2 * (p0 + (int64_t)s * d.rows)]);
-  float Ltot = 0.0f;
-  float o[PER];
-#pragma unroll
-  for (int e = 0; e < PER; ++e) o[e] = 0.0f;
-  for (int s = 0; s < d.splits; ++s) {
-    const int64_t p = p0 + (int64_t)s * d.rows;
-    const float ms = d.part_ml[2 * p];
-    const float f = (ms == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-    Ltot += f * d.part_ml[2 * p + 1];
-#pragma unroll
-    for (int e = 0; e < PER; ++e) o[e] += f * d.part_o[p * D + lane + 64 * e];
+  // maximum over the splits
+  float m = -__builtin_inff();
+  for (int s = tid; s < S; s += kCombineThreads) {
+    const float ms = d.part_ml[2 * (p0 + (int64_t)s * d.rows)];
+    w_s[s] = ms;
+    m = fmaxf(m, ms);
   }
-  const float inv = (Ltot > 0.0f) ? (1.0f / Ltot) : 0.0f;
-  _Float16* op = a.o + b * a.osb + hq * a.osh + (int64_t)qi * a.osn;
+  red[tid] = m;
+  __syncthreads();
+  for (int off = kCombineThreads / 2; off > 0; off >>= 1) {
+    if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
+    __syncthreads();
+  }
+  const float M = red[0];
+  __syncthreads();
+  // weights and the weighted sum of l
+  float lsum = 0.0f;
+  for (int s = tid; s < S; s += kCombineThreads) {
+    const float ms = w_s[s];
+    const float w = (ms == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+    w_s[s] = w;
+    lsum += w * d.part_ml[2 * (p0 + (int64_t)s * d.rows) + 1];
+  }
+  red[tid] = lsum;
+  __syncthreads();
+  for (int off = kCombineThreads / 2; off > 0; off >>= 1) {
+    if (tid < off) red[tid] += red[tid + off];
+    __syncthreads();
+  }
+  const float Ltot = red[0];
+
+  // weighted O: group grp handles splits grp, grp + GROUPS, ...
+  const int dim = tid % D;
+  const int grp = tid / D;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int s = grp;
+  for (; s + 3 * GROUPS < S; s += 4 * GROUPS) {
 #pragma unroll
-  for (int e = 0; e < PER; ++e) op[lane + 64 * e] = (_Float16)(o[e] * inv);
-  if (a.lse != nullptr && lane == 0) {
+    for (int u = 0; u < 4; ++u) {
+      const int su = s + u * GROUPS;
+      acc[u] += w_s[su] * d.part_o[(p0 + (int64_t)su * d.rows) * D + dim];
+    }
+  }
+  for (; s < S; s += GROUPS) acc[0] += w_s[s] * d.part_o[(p0 + (int64_t)s * d.rows) * D + dim];
+  o_part[grp][dim] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+  if (grp != 0) return;
+  float o = 0.0f;
+#pragma unroll
+  for (int q = 0; q < GROUPS; ++q) o += o_part[q][dim];
+  const float inv = (Ltot > 0.0f) ? (1.0f / Ltot) : 0.0f;
+  a.o[b * a.osb + hq * a.osh + (int64_t)qi * a.osn + dim] = (_Float16)(o * inv);
+  if (a.lse != nullptr && dim == 0) {
     const float m_use = (M == -__builtin_inff()) ? 0.0f : M;
     a.lse[((int64_t)b * a.hq + hq) * a.n + qi] =
         (m_use + __builtin_log2f(Ltot)) * 0.69314718055994530942f;
@@ -383,7 +428,7 @@ DecodePlan plan_decode(const FwdArgs& a, int batch, int head_dim, bool causal,
   int64_t nk_eff = a.nk;
   if (causal) nk_eff = std::min<int64_t>(a.nk, std::max<int64_t>(0, (int64_t)a.n + a.diag));
   pl.tiles = (int)((nk_eff + kDecTile - 1) / kDecTile);
-  int splits = (kDecTargetWgs + pl.units - 1) / pl.units;
+  int splits = std::min((kDecTargetWgs + pl.units - 1) / pl.units, kMaxSplits);
   splits = std::min(splits, std::max(1, pl.tiles / kDecMinTiles));
   splits = std::max(splits, 1);
   pl.chunk_tiles = std::max(1, (pl.tiles + splits - 1) / splits);
@@ -421,9 +466,9 @@ int launch_decode_forward(const FwdArgs& a, const DecodePlan& pl, int head_dim, 
   if (pl.splits > 1) {
     const dim3 cgrid((unsigned)((int64_t)pl.units * pl.rows));
     if (head_dim == 128)
-      hipLaunchKernelGGL(fa_decode_combine<128>, cgrid, dim3(64), 0, stream, d);
+      hipLaunchKernelGGL(fa_decode_combine<128>, cgrid, dim3(kCombineThreads), 0, stream, d);
     else
-      hipLaunchKernelGGL(fa_decode_combine<64>, cgrid, dim3(64), 0, stream, d);
+      hipLaunchKernelGGL(fa_decode_combine<64>, cgrid, dim3(kCombineThreads), 0, stream, d);
   }
   return 0;
 }
