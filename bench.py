@@ -195,6 +195,32 @@ def time_decode(name, steps=20, warmup=5, policy=0):
     return ms, nbytes / (ms * 1e-3) / 1e9
 
 
+def time_sdpa_decode_call(keys, n=200):
+    """One decode-step SDPA call with transformers' layouts (Q a [B,1,H,D]
+    projection viewed as [B,H,1,D], a contiguous [B,Hkv,L,D] cache), Qwen2-0.5B
+    heads: torch's SDPA vs the patched call, HIP events around n calls."""
+    import torch
+
+    from flash_attention_sm75 import sdpa_patch
+
+    g = torch.Generator("cpu").manual_seed(3)
+    q = torch.randn(1, 1, 14 * 64, generator=g).half().cuda().view(1, 1, 14, 64).transpose(1, 2)
+    k = torch.randn(1, 2, keys, 64, generator=g).half().cuda()
+    v = torch.randn(1, 2, keys, 64, generator=g).half().cuda()
+    out = {}
+    for name, fn in (("torch", sdpa_patch._original_sdpa), ("patched", sdpa_patch._patched_sdpa)):
+        for _ in range(20):
+            fn(q, k, v, enable_gqa=True)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn(q, k, v, enable_gqa=True)
+        b.record()
+        torch.cuda.synchronize()
+        out[name] = a.elapsed_time(b) / n * 1e3
+    return out
+
+
 def time_hf(prompt_len=4096, decode_steps=32):
     """Random-init Qwen2-0.5B-shaped model (no weights can be downloaded):
     prefill and teacher-forced KV-cache decode, unpatched vs patched SDPA."""
@@ -301,6 +327,10 @@ def main():
                 f"128-row prefill kernel {ms_pre:.4f} ms ({gbs_pre:.0f} GB/s)")
 
     if args.hf:
+        for keys in (4097, 32769):
+            t = time_sdpa_decode_call(keys)
+            log(f"[sdpa-decode-call] {keys} keys, Qwen2-0.5B heads: torch {t['torch']:.1f} us, "
+                f"patched {t['patched']:.1f} us per call")
         r = time_hf()
         (pu, du), (pp, dp) = r["unpatched"], r["patched"]
         log(f"[hf] Qwen2-0.5B shape, random init, prompt 4096: prefill {pu * 1e3:.1f} ms -> "
