@@ -284,6 +284,8 @@ def main():
     ap.add_argument("--hf", action="store_true",
                     help="also time a random-init Qwen2-0.5B-shaped model, unpatched vs "
                          "patched SDPA (stderr)")
+    ap.add_argument("--policy", type=int, default=0, choices=(0, 1, 2),
+                    help="kernel policy: 0 auto, 1 = 128-row (4-wave), 2 = 256-row (8-wave)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise copy of 256 MiB (known HBM bytes) "
                          "to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
@@ -298,6 +300,10 @@ def main():
 
     cfg = args.config
     B, Hq, Hkv, N, D, causal, _, _ = CONFIGS[cfg]
+    if args.policy:
+        import flash_attn_sm75_cuda as _C
+
+        _C.set_kernel_policy(args.policy)
     F = flops(B, Hq, N, D, causal)
 
     if args.copy_calibration:

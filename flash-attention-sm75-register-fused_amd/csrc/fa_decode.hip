@@ -258,6 +258,9 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   }
 
   // ---- merge the four waves through LDS (the V tiles are free now) --------
+  // The last step's loads of a tile that does not exist are still in flight:
+  // drain them, or their zeros could land in LDS after the merge writes.
+  wait_vmcnt<0>();
   const float l_tot = halves_sum(l_run);
   __syncthreads();
   {

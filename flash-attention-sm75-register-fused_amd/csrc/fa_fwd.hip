@@ -53,14 +53,20 @@
 namespace fa {
 namespace {
 
-// Software-pipelined main loop: iteration j computes S^T_{j+1} = K_{j+1} Q^T
-// while the VALU turns S^T_j into probabilities, then accumulates P_j V_j.
-// LDS holds two K and two V tiles; the direct loads of K_{j+2} and V_{j+1}
-// issued during iteration j land in the buffers iteration j-1 freed, so one
-// barrier per iteration suffices.  KV_SAME_STRIDE: K and V rows have the
-// same stride, so V's direct-load offsets are K's (saves registers).
-template <int D, bool CAUSAL, bool KV_SAME_STRIDE>
-__global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
+// Software-pipelined main loop: step j computes S^T_{j+1} = K_{j+1} Q^T while
+// the VALU turns S^T_j into probabilities, then accumulates P_j V_j.  One
+// barrier per step.  Two shapes (WAVES):
+//   * 4 waves, 128 query rows, two workgroups per CU, K/V tiles double
+//     buffered (STAGES = 2): step j loads K_{j+2} and V_{j+1} into the
+//     buffers step j-1 freed, and they must land by the end of step j;
+//   * 8 waves, 256 query rows, one workgroup per CU, triple buffered
+//     (STAGES = 3): step j loads K_{j+3} and V_{j+2}, which have until the
+//     end of step j+1 to land; every K/V tile serves 256 query rows, and each
+//     wave issues half as many direct loads (waves 0-3 load K, 4-7 load V).
+// KV_SAME_STRIDE: K and V rows have the same stride, so the direct-load
+// offsets are shared (saves registers).
+template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
   using L = Lds<D>;
   constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
   constexpr int MT = D / 32;       // 32-row output tiles of O^T
@@ -68,21 +74,32 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   constexpr int NPV = 4 * MT;      // P V MFMAs per tile
   constexpr int PFK = 3;           // K operand reads run this many MFMAs ahead
   constexpr int PFV = 2;           // V operand reads run this many MFMAs ahead
-  constexpr int SEGW = L::SegsPerWave;
+  constexpr int BLOCK_M = 32 * WAVES;
+  constexpr int STAGES = WAVES == 8 ? 3 : 2;
+  constexpr int SEGQ = L::Segs / 4;           // segments of one tile per wave quarter
+  constexpr int LPW = 2 * L::Segs / WAVES;    // direct loads per wave per step
+  constexpr bool SPLIT_ROLES = WAVES == 8;    // a wave loads K or V, not both
+  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
+  static_assert(L::Segs % 4 == 0, "tile segments must split over 4 waves");
 
-  // [K buffer 0 | K buffer 1 | V buffer 0 | V buffer 1]
-  // Four distinct objects (not one array): the loop is unrolled by two, so
-  // every access names its buffer at compile time and the compiler can see
-  // that the in-flight direct loads never alias the tiles being read (it
-  // would otherwise drain vmcnt before each LDS read).
+  // STAGES K buffers and STAGES V buffers, distinct objects (not one array):
+  // the loop is unrolled by STAGES, so every access names its buffer at
+  // compile time and the compiler can see that the in-flight direct loads
+  // never alias the tiles being read (it would otherwise drain vmcnt before
+  // each LDS read).
   __shared__ __attribute__((aligned(1024))) _Float16 k_lds0[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 k_lds1[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds2[STAGES == 3 ? L::Tile : 1];
   __shared__ __attribute__((aligned(1024))) _Float16 v_lds0[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 v_lds1[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds2[STAGES == 3 ? L::Tile : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // Scalar: the direct loads' LDS destinations (M0) derive from it.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wq = wave & 3;    // quarter of the direct-load segments
+  const bool v_role = SPLIT_ROLES && wave >= 4;
   const int hi = lane >> 5;   // which half of the wave
   const int ql = lane & 31;   // query column owned by this lane
   const int grp = lane >> 4;  // 16-lane group (transposing reads)
@@ -91,7 +108,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const Work w = block_work(a, (int)blockIdx.x, CAUSAL);
   const int b = w.b, hq = w.hq, hkv = w.hkv, qb = w.qb;
   const int bh = b * a.hq + hq;
-  const int q0 = qb * kBlockM;
+  const int q0 = qb * BLOCK_M;
   const int qw = q0 + wave * 32;
   const int qrow = qw + ql;
   const int N = a.n;    // query rows
@@ -117,26 +134,30 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   }
 
   // Keys this block can see (none for a block entirely before the diagonal).
-  const int kv_len = CAUSAL ? max(0, min(NK, q0 + kBlockM + a.diag)) : NK;
+  const int kv_len = CAUSAL ? max(0, min(NK, q0 + BLOCK_M + a.diag)) : NK;
   const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
 
-  // Direct-load map: wave w fills 1 KB segments w, w + 4, ...; lane l of a
-  // segment covers tile bytes [1024 seg + 16 l, +16).  Precompute the global
-  // byte offset inside a tile for each segment (padding lanes: past the end).
-  int goff_k[SEGW], goff_v_own[KV_SAME_STRIDE ? 1 : SEGW];
-  int* goff_v = KV_SAME_STRIDE ? goff_k : goff_v_own;
+  // Direct-load map: wave quarter wq fills 1 KB segments wq, wq + 4, ... of a
+  // tile; lane l of a segment covers tile bytes [1024 seg + 16 l, +16).  The
+  // global byte offset inside a tile of each segment (padding lanes: past
+  // the end).  goff_a: K (4 waves) or this wave's tile kind (8 waves);
+  // goff_b: V with its own stride (4 waves, different strides only).
+  constexpr bool OWN_B = !SPLIT_ROLES && !KV_SAME_STRIDE;
+  int goff_a[SEGQ], goff_b_own[OWN_B ? SEGQ : 1];
+  int* goff_b = OWN_B ? goff_b_own : goff_a;
+  const int64_t a_stride = v_role ? a.vsn : a.ksn;
 #pragma unroll
-  for (int s = 0; s < SEGW; ++s) {
-    const int pos = (wave + kWaves * s) * 1024 + 16 * lane;  // bytes into the tile
+  for (int s = 0; s < SEGQ; ++s) {
+    const int pos = (wq + 4 * s) * 1024 + 16 * lane;  // bytes into the tile
     const int row = pos / (2 * L::Pitch);
     const int within = pos - row * (2 * L::Pitch);
     if (within < 2 * D) {
       const int c = (within >> 4) ^ ((row >> 2) & 3);
-      goff_k[s] = (int)(row * a.ksn * 2) + 16 * c;
-      if (!KV_SAME_STRIDE) goff_v[s] = (int)(row * a.vsn * 2) + 16 * c;
+      goff_a[s] = (int)(row * a_stride * 2) + 16 * c;
+      if (OWN_B) goff_b[s] = (int)(row * a.vsn * 2) + 16 * c;
     } else {
-      goff_k[s] = -16;  // 0xfffffff0: beyond any window -> writes zeros
-      if (!KV_SAME_STRIDE) goff_v[s] = -16;
+      goff_a[s] = -16;  // 0xfffffff0: beyond any window -> writes zeros
+      if (OWN_B) goff_b[s] = -16;
     }
   }
   const int k_tile_bytes = (int)(kBlockN * a.ksn * 2);
@@ -144,15 +165,17 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const int k_all_bytes = (int)(NK * a.ksn * 2);
   const int v_all_bytes = (int)(NK * a.vsn * 2);
 
-  // Buffer selection by compile-time parity.
-  auto kbuf = [&](auto par) -> _Float16* {
-    if constexpr (decltype(par)::value) return k_lds1; else return k_lds0;
+  // Buffer selection by compile-time stage index.
+  auto kbuf = [&](auto st) -> _Float16* {
+    constexpr int S = decltype(st)::value % STAGES;
+    if constexpr (S == 0) return k_lds0; else if constexpr (S == 1) return k_lds1; else return k_lds2;
   };
-  auto vbuf = [&](auto par) -> _Float16* {
-    if constexpr (decltype(par)::value) return v_lds1; else return v_lds0;
+  auto vbuf = [&](auto st) -> _Float16* {
+    constexpr int S = decltype(st)::value % STAGES;
+    if constexpr (S == 0) return v_lds0; else if constexpr (S == 1) return v_lds1; else return v_lds2;
   };
   auto lds_seg = [&](_Float16* tile, int s) -> lds_void* {
-    return (lds_void*)(tile + (wave + kWaves * s) * 512);
+    return (lds_void*)(tile + (wq + 4 * s) * 512);
   };
   // Buffer windows of tile j (empty past the last tile: every lane reads 0).
   auto k_window = [&](int j) {
@@ -163,19 +186,12 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
     const int bytes = v_all_bytes - j * v_tile_bytes;
     return make_rsrc(Vp + (int64_t)j * kBlockN * a.vsn, bytes > 0 ? bytes : 0);
   };
-  auto load_k = [&](int j, _Float16* dst) {
-    const __amdgpu_buffer_rsrc_t r =
-        make_rsrc(Kp + (int64_t)j * kBlockN * a.ksn, k_all_bytes - j * k_tile_bytes);
+  // This wave's segments of K tile j (into kdst) or V tile j (into vdst).
+  auto load_tile = [&](bool is_v, int j, _Float16* dst) {
+    const __amdgpu_buffer_rsrc_t r = is_v ? v_window(j) : k_window(j);
 #pragma unroll
-    for (int s = 0; s < SEGW; ++s)
-      direct_load16(r, lds_seg(dst, s), goff_k[s]);
-  };
-  auto load_v = [&](int j, _Float16* dst) {
-    const __amdgpu_buffer_rsrc_t r =
-        make_rsrc(Vp + (int64_t)j * kBlockN * a.vsn, v_all_bytes - j * v_tile_bytes);
-#pragma unroll
-    for (int s = 0; s < SEGW; ++s)
-      direct_load16(r, lds_seg(dst, s), goff_v[s]);
+    for (int s = 0; s < SEGQ; ++s)
+      direct_load16(r, lds_seg(dst, s), (is_v && OWN_B) ? goff_b[s] : goff_a[s]);
   };
 
   // Per-lane LDS bases of the operand reads (see Lds): K rows ql (+32t),
@@ -211,8 +227,9 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
   const float c2 = a.c;  // |scale| * log2(e)
   const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-  // S^T of two tiles in flight, ping-pong by tile parity (no copies): the
-  // step for tile j reads s_buf[j & 1] and fills s_buf[(j + 1) & 1].
+  // S^T of two tiles in flight, ping-pong by the parity of the step's
+  // position in the unrolled loop: step u reads s_buf[u & 1] and fills the
+  // other one (with three stages, one copy per three steps restores it).
   float16v s_buf[2][2];
   auto row_max = [](const float16v (&s)[2]) {
     float m0 = s[0][0], m1 = s[1][0];
@@ -259,33 +276,40 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
     mc = ((m_run == -__builtin_inff()) ? 0.0f : m_run) * c2;
   };
 
-  // One pipeline step for tile j (PAR = j & 1), whose scores are prepared.
-  // HAS_NEXT: tile j+1 exists, so S_{j+1} is computed (and prepared) here
-  // and the loads of V_{j+1} (and K_{j+2}) are issued.
-  auto step = [&](int j, auto has_next_t, auto par_t) {
+  // One pipeline step for tile j, at position U of the unrolled loop (its
+  // V tile is in buffer U % STAGES), whose scores are prepared.  HAS_NEXT:
+  // tile j+1 exists, so S_{j+1} is computed (and prepared) here and the
+  // loads of K_{j+STAGES} and V_{j+STAGES-1} are issued.
+  auto step = [&](int j, auto has_next_t, auto u_t) {
     constexpr bool HAS_NEXT = decltype(has_next_t)::value;
-    constexpr bool PAR = decltype(par_t)::value;
+    constexpr int U = decltype(u_t)::value;
+    constexpr int PAR = U & 1;
     constexpr int ns = HAS_NEXT ? NS : 0;     // S MFMAs this step
-    const _Float16* Kn = kbuf(Flag<!PAR>{});
-    const _Float16* Vc = vbuf(Flag<PAR>{});
-    float16v (&s_cur)[2] = s_buf[PAR ? 1 : 0];
-    float16v (&s_nxt)[2] = s_buf[PAR ? 0 : 1];
+    const _Float16* Kn = kbuf(std::integral_constant<int, U + 1>{});
+    const _Float16* Vc = vbuf(std::integral_constant<int, U>{});
+    float16v (&s_cur)[2] = s_buf[PAR];
+    float16v (&s_nxt)[2] = s_buf[1 - PAR];
 
-    // Direct loads of K_{j+2} (empty window past the end) and V_{j+1}, one
-    // 1 KB segment after each of the first MFMAs, so the address unit's
-    // queueing overlaps MFMA execution.
+    // Direct loads of K_{j+STAGES} (into the buffer K_j used) and
+    // V_{j+STAGES-1} (into the buffer V_{j-1} used), one 1 KB segment after
+    // each of the first MFMAs, so the address unit's queueing overlaps MFMA
+    // execution.  Past the last tile the windows are empty.
     __amdgpu_buffer_rsrc_t rk_next, rv_next;
     if (HAS_NEXT) {
-      rk_next = k_window(j + 2);
-      rv_next = v_window(j + 1);
+      rk_next = k_window(j + STAGES);
+      rv_next = v_window(j + STAGES - 1);
     }
-    _Float16* k_dst = kbuf(Flag<PAR>{});
-    _Float16* v_dst = vbuf(Flag<!PAR>{});
-    auto issue_load = [&](int q) {  // q < SEGW: K segment q, else V segment q - SEGW
-      if (q < SEGW)
-        direct_load16(rk_next, lds_seg(k_dst, q), goff_k[q]);
-      else
-        direct_load16(rv_next, lds_seg(v_dst, q - SEGW), goff_v[q - SEGW]);
+    _Float16* k_dst = kbuf(std::integral_constant<int, U>{});
+    _Float16* v_dst = vbuf(std::integral_constant<int, U + STAGES - 1>{});
+    auto issue_load = [&](int q) {
+      if constexpr (SPLIT_ROLES) {  // q < SEGQ: segment q of this wave's tile kind
+        direct_load16(v_role ? rv_next : rk_next, lds_seg(v_role ? v_dst : k_dst, q), goff_a[q]);
+      } else {  // q < SEGQ: K segment q, else V segment q - SEGQ
+        if (q < SEGQ)
+          direct_load16(rk_next, lds_seg(k_dst, q), goff_a[q]);
+        else
+          direct_load16(rv_next, lds_seg(v_dst, q - SEGQ), goff_b[q - SEGQ]);
+      }
     };
 
     // ---- slots: S_{j+1} MFMAs, then P_j V_j --------------------------------
@@ -354,9 +378,9 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
         oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[v], pf[ks], oacc[mt], 0, 0, 0);
       }
       if constexpr (HAS_NEXT) {
-        static_for<2 * SEGW>([&](auto q_c) {
+        static_for<LPW>([&](auto q_c) {
           constexpr int q = decltype(q_c)::value;
-          if constexpr ((q * (NB / 2)) / (2 * SEGW) == slot) issue_load(q);
+          if constexpr ((q * (NB / 2)) / LPW == slot) issue_load(q);
         });
         static_for<32>([&](auto e_c) {
           constexpr int e = decltype(e_c)::value;
@@ -372,17 +396,23 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
 
     if (HAS_NEXT) {
       prepare(j + 1, s_nxt, mx_next);
-      barrier_after_direct_loads();  // V_{j+1}, K_{j+2} landed; V_j, K_{j+1} reads done
+      // The loads of the previous step have landed (those of this step may
+      // still be in flight with three stages), and every wave is done with
+      // the buffers the next step's loads overwrite.
+      barrier_after_loads<STAGES == 3 ? LPW : 0>();
     }
   };
 
-  // ---- prologue: K_0, V_0, K_1 into LDS; S_0 -------------------------------
+  // ---- prologue: K_0..K_{STAGES-1} and V_0..V_{STAGES-2} into LDS; S_0 -----
   if (ntiles > 0) {
-    load_k(0, k_lds0);
-    load_v(0, v_lds0);
-    if (ntiles > 1) load_k(1, k_lds1);
+    static_for<STAGES>([&](auto t_c) {
+      if (!v_role) load_tile(false, decltype(t_c)::value, kbuf(t_c));
+    });
+    static_for<STAGES - 1>([&](auto t_c) {
+      if (!SPLIT_ROLES || v_role) load_tile(true, decltype(t_c)::value, vbuf(t_c));
+    });
   }
-  barrier_after_direct_loads();
+  barrier_after_loads<0>();
   if (ntiles > 0) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -393,18 +423,36 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
                                                              s_buf[0][t], 0, 0, 0);
     }
     prepare(0, s_buf[0], halves_max(row_max(s_buf[0])));
+    // Step 0 loads K_STAGES into K_0's buffer: every wave must be done
+    // reading it for S_0 first.
+    __syncthreads();
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
     int j = 0;
-    for (; j + 2 < ntiles; j += 2) {
-      step(j, Flag<true>{}, Flag<false>{});
-      step(j + 1, Flag<true>{}, Flag<true>{});
+    for (; j + STAGES < ntiles; j += STAGES) {  // every step has a next tile
+      step(j, Flag<true>{}, I0{});
+      step(j + 1, Flag<true>{}, I1{});
+      if constexpr (STAGES == 3) {
+        step(j + 2, Flag<true>{}, I2{});
+        s_buf[0][0] = s_buf[1][0];
+        s_buf[0][1] = s_buf[1][1];
+      }
     }
-    if (j + 1 < ntiles) {
-      step(j, Flag<true>{}, Flag<false>{});
-      step(j + 1, Flag<false>{}, Flag<true>{});
-    } else {
-      step(j, Flag<false>{}, Flag<false>{});
+    const int rest = ntiles - j;  // 1 .. STAGES steps left, the last one without a next tile
+    if (rest == 1) {
+      step(j, Flag<false>{}, I0{});
+    } else if (STAGES == 2 || rest == 2) {
+      step(j, Flag<true>{}, I0{});
+      step(j + 1, Flag<false>{}, I1{});
+    } else if constexpr (STAGES == 3) {
+      step(j, Flag<true>{}, I0{});
+      step(j + 1, Flag<true>{}, I1{});
+      step(j + 2, Flag<false>{}, I2{});
     }
   }
+  // No direct load may land in LDS after the workgroup ends.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 
   // ---- epilogue: combine the two half-wave partial sums, normalise, store ---
   const float l_tot = halves_sum(l_run);
@@ -431,27 +479,16 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(const FwdArgs a) {
 
 }  // namespace
 
-// Whether the automatic policy may pick the 256-row kernel.  Off: it needs
-// more than the 512 registers per lane a wave can hold and spills, so it is
-// only reachable through FA_POLICY_WIDE.
-constexpr bool kAutoWide = false;
+namespace {
 
-int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
-                         int policy, hipStream_t stream) {
+template <int WAVES>
+void launch_waves(const FwdArgs& a, int batch, int head_dim, bool causal, hipStream_t stream) {
   const bool same = a.ksn == a.vsn;
-  const dim3 block(kThreads);
-  // The wide kernel (256 rows per workgroup, one workgroup per CU) when there
-  // are enough workgroups to give every CU at least two.  It assumes a
-  // non-negative scale (the narrow kernel negates Q for the other case).
-  const int64_t wide_blocks = ((int64_t)a.n + kBlockMWide - 1) / kBlockMWide;
-  const bool wide = head_dim == 128 && !a.negate_q &&
-                    (policy == 2 || (policy == 0 && kAutoWide &&
-                                     (int64_t)batch * a.hq * wide_blocks >= 512));
-  if (wide) return launch_fused_forward_wide(a, batch, causal, stream);
   FwdArgs args = a;
-  const dim3 grid((unsigned)plan_grid(args, batch, kBlockM));
+  const dim3 grid((unsigned)plan_grid(args, batch, 32 * WAVES));
+  const dim3 block(64 * WAVES);
 #define FA_LAUNCH(D, C, S) \
-  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S>), grid, block, 0, stream, args)
+  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES>), grid, block, 0, stream, args)
   if (head_dim == 128) {
     if (causal) {
       if (same) FA_LAUNCH(128, true, true); else FA_LAUNCH(128, true, false);
@@ -466,6 +503,20 @@ int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
     }
   }
 #undef FA_LAUNCH
+}
+
+}  // namespace
+
+// The 8-wave (256-row, one workgroup per CU) kernel only runs when asked
+// for (FA_POLICY_WIDE): measured on C4 it is ~4% slower than the 4-wave
+// kernel -- with one workgroup per CU both waves of a SIMD stop at the same
+// barrier, where two independent 4-wave workgroups cover each other's.
+int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
+                         int policy, hipStream_t stream) {
+  if (policy == 2)
+    launch_waves<8>(a, batch, head_dim, causal, stream);
+  else
+    launch_waves<4>(a, batch, head_dim, causal, stream);
   return 0;
 }
 

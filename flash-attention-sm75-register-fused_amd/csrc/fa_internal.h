@@ -34,15 +34,11 @@ struct FwdArgs {
 };
 
 // Launches the fused MFMA kernel; all arguments already validated.
-// policy: 0 = choose by problem size, 1 = 128-row workgroups (two waves per
-// SIMD), 2 = 256-row workgroups (one wave per SIMD, head_dim 128 only).
+// policy: 0 = automatic and 1 = 128-row workgroups of 4 waves (two per CU),
+// 2 = 256-row workgroups of 8 waves (one per CU, K/V triple-buffered).
 int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
                          int policy, hipStream_t stream);
-
-// 256-row workgroups (head_dim 128, scale >= 0); called by the above.
-constexpr int kBlockMWide = 256;
-int launch_fused_forward_wide(const FwdArgs& a, int batch, bool causal, hipStream_t stream);
-int fused_block_m();
+int fused_block_m();  // rows of the smallest workgroup (grid-size checks)
 
 // Split-K path for few query rows per K/V head (fa_decode.hip): taken when
 // heads_q / heads_kv * seq_len <= kDecodeMaxRows.

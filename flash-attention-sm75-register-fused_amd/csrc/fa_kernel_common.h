@@ -1,5 +1,5 @@
 // Device-side building blocks shared by the fused attention kernels
-// (fa_fwd.hip: 128-row workgroups; fa_fwd_wide.hip: 256-row workgroups).
+// (fa_fwd.hip: prefill, fa_decode.hip: split-K decode).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -47,8 +47,7 @@ struct Lds {
   static constexpr int Pitch = D + 32;           // halves per row
   static constexpr int Tile = kBlockN * Pitch;   // halves per K (or V) tile
   static constexpr int Segs = Tile * 2 / 1024;   // 1 KB direct-load segments
-  static constexpr int SegsPerWave = Segs / kWaves;
-  static_assert(Segs % kWaves == 0, "segments must split over the waves");
+  static_assert(Segs % 4 == 0, "segments must split over 4 waves");
 };
 
 __device__ __forceinline__ half4 ds_read_tr16(const _Float16* p) {
@@ -86,11 +85,14 @@ __device__ __forceinline__ void direct_load16(__amdgpu_buffer_rsrc_t r, lds_void
 // Freezes the instruction order at this point (nothing is moved across).
 __device__ __forceinline__ void fence_schedule() { __builtin_amdgcn_sched_barrier(0); }
 
-// Workgroup barrier that also publishes this wave's direct-to-LDS loads:
-// they are counted by vmcnt, which the compiler does not drain before
-// s_barrier on its own.  0x0F70 = vmcnt(0) expcnt(7) lgkmcnt(15) (gfx9).
-__device__ __forceinline__ void barrier_after_direct_loads() {
-  __builtin_amdgcn_s_waitcnt(0x0F70);
+// Workgroup barrier after which all but this wave's last N direct-to-LDS
+// loads have landed (vmcnt counts them, and they complete in order), so the
+// tiles they wrote are visible to every wave.  The compiler does not wait
+// for direct loads before s_barrier on its own.
+template <int N>
+__device__ __forceinline__ void barrier_after_loads() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
   __syncthreads();
 }
 

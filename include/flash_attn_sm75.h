@@ -122,9 +122,9 @@ int fa_sm75_abi_version(void);
 /* Fused-kernel selection, process-wide (no reference counterpart: a tuning
  * and testing control).  AUTO picks by problem size (the split-K path for
  * few query rows per K/V head, else 128-row workgroups); NARROW forces
- * 128-row workgroups (two waves per SIMD); WIDE forces 256-row workgroups
- * (one wave per SIMD, 64 rows per wave; head_dim 128 only, head_dim 64 stays
- * NARROW).  All kernels compute the same function. */
+ * 128-row workgroups of 4 waves (two workgroups per CU); WIDE forces 256-row
+ * workgroups of 8 waves (one per CU, K/V tiles triple-buffered).  All
+ * kernels compute the same function. */
 enum fa_kernel_policy { FA_POLICY_AUTO = 0, FA_POLICY_NARROW = 1, FA_POLICY_WIDE = 2 };
 int fa_sm75_set_kernel_policy(int policy); /* FA_OK or FA_ERR_INVALID_ARGUMENT */
 int fa_sm75_get_kernel_policy(void);

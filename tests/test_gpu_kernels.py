@@ -1,10 +1,11 @@
-"""Both fused kernels against the oracle on the same inputs (needs a GPU).
+"""Both fused kernel shapes against the oracle on the same inputs (needs a GPU).
 
-fa_sm75_forward picks between a 128-row workgroup kernel (two waves per
-SIMD) and a 256-row one (one wave per SIMD, 64 rows per wave, head_dim 128)
-by problem size; fa_sm75_set_kernel_policy forces either, so each is checked
-on the shapes the other would normally take.  Tolerance as in
-test_gpu_parity: |O - O_ref| <= 2e-3 + 1e-2 |O_ref|.
+The prefill kernel comes as 128-row workgroups of 4 waves (two per CU, K/V
+double-buffered; the automatic choice) and 256-row workgroups of 8 waves (one
+per CU, K/V triple-buffered); fa_sm75_set_kernel_policy forces either, so
+each is checked on the same shapes, including the tails and 1-row cases the
+split-K path would otherwise take.  Tolerance as in test_gpu_parity:
+|O - O_ref| <= 2e-3 + 1e-2 |O_ref|.
 """
 import contextlib
 import ctypes
@@ -60,6 +61,8 @@ SHAPES = [
     (1, 4, 4, 700, 128, False),
     (1, 3, 1, 1030, 128, True),
     (1, 2, 2, 300, 64, True),
+    (2, 4, 2, 777, 64, False),
+    (1, 8, 8, 1100, 64, True),
 ]
 
 
