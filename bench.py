@@ -93,7 +93,7 @@ def read_traffic(cfg):
     return float(m.group(1)) if m else None
 
 
-def time_gpu(cfg, steps, warmup):
+def time_gpu(cfg, steps, warmup, data="randn"):
     import torch
 
     from flash_attention_sm75 import flash_attention_forward
@@ -101,6 +101,8 @@ def time_gpu(cfg, steps, warmup):
     B, Hq, Hkv, N, D, causal, _, _ = CONFIGS[cfg]
     dev = torch.device("cuda", 0)
     q, k, v = (t.to(dev) for t in make_inputs(cfg))
+    if data == "zeros":  # same launches, no data toggling: shows the power limit
+        q, k, v = (torch.zeros_like(t) for t in (q, k, v))
     torch.cuda.synchronize()
     for _ in range(warmup):
         flash_attention_forward(q, k, v, causal=causal)
@@ -284,6 +286,9 @@ def main():
     ap.add_argument("--hf", action="store_true",
                     help="also time a random-init Qwen2-0.5B-shaped model, unpatched vs "
                          "patched SDPA (stderr)")
+    ap.add_argument("--data", default="randn", choices=("randn", "zeros"),
+                    help="diagnostic: 'zeros' times the same launches on all-zero inputs "
+                         "(the kernel is power-limited: less data toggling, higher clock)")
     ap.add_argument("--policy", type=int, default=0, choices=(0, 1, 2),
                     help="kernel policy: 0 auto, 1 = 128-row (4-wave), 2 = 256-row (8-wave)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -343,7 +348,7 @@ def main():
             f"{pp * 1e3:.1f} ms patched; decode {du * 1e3:.2f} -> {dp * 1e3:.2f} ms/token; "
             f"patch stats {r['stats']}")
 
-    wall, kern_ms = time_gpu(cfg, args.steps, args.warmup)
+    wall, kern_ms = time_gpu(cfg, args.steps, args.warmup, args.data)
     ms_per_step = wall * 1e3 / args.steps
     avg_kernel_ms = sum(kern_ms) / len(kern_ms)
     value = F * args.steps / wall / 1e12
@@ -370,7 +375,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic (seeded CPU generator, N(0,1) fp16, resident in HBM)",
+        "data": ("synthetic (seeded CPU generator, N(0,1) fp16, resident in HBM)"
+                 if args.data == "randn" else "DIAGNOSTIC all-zero inputs (not the metric)"),
         "config": {
             "workload": f"{cfg}: {DESCR[cfg]}",
             "batch": B, "heads_q": Hq, "heads_kv": Hkv, "seq_len": N, "head_dim": D,
