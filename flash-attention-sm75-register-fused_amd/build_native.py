@@ -29,7 +29,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIP_LIB_NAME = "libflash_attn_sm75_hip.so"
 EXT_NAME = "flash_attn_sm75_cuda"
 
-HIP_SOURCES = ["fa_fwd.hip", "fa_decode.hip", "fa_naive.hip", "fa_capi.hip"]
+HIP_SOURCES = ["fa_fwd.hip", "fa_decode.hip", "fa_mask.hip", "fa_naive.hip", "fa_capi.hip"]
 
 # Packed-FP32 VALU forms are disabled for all device code.
 HIPCC_FLAGS = [

@@ -8,7 +8,8 @@
 // Additions: flash_attention_forward accepts grouped K/V heads (Hkv divides
 // Hq) so no repeat_interleave copy is needed, flash_attention_forward_lse
 // also returns the fp32 row log-sum-exp, and flash_attention_forward_ex takes
-// strided views in place, Nq != Nk and either causal alignment.
+// strided views in place, Nq != Nk, either causal alignment and a boolean
+// attn_mask.
 //
 // All checks run before any device work; the kernels are enqueued on the
 // current HIP stream of Q's device and the host is not blocked.
@@ -149,9 +150,35 @@ int64_t eff_stride(const torch::Tensor& t, int i, int64_t fallback) {
   return t.size(i) == 1 ? fallback : t.stride(i);
 }
 
+// Packs a boolean mask broadcastable to [B, Hq, Nq, Nk] into bit rows; the
+// mask's own size-1 (or stride-0) batch, head and query dimensions stay size
+// 1 in the packed tensor and get stride 0 in the params.
+torch::Tensor pack_mask(const torch::Tensor& mask, const torch::Tensor& Q, int64_t nk,
+                        fa_fwd_params& p) {
+  TORCH_CHECK(mask.dtype() == torch::kBool, "attn_mask must be a bool tensor");
+  TORCH_CHECK(mask.device() == Q.device(), "attn_mask must be on Q's device");
+  TORCH_CHECK(mask.dim() <= 4, "attn_mask must have at most 4 dimensions");
+  const auto m = mask.expand({Q.size(0), Q.size(1), Q.size(2), nk});
+  int64_t own[3];
+  for (int d = 0; d < 3; ++d) own[d] = (m.size(d) == 1 || m.stride(d) == 0) ? 1 : m.size(d);
+  const int64_t words = (nk + 63) / 64;
+  auto bits = torch::empty({own[0], own[1], own[2], words}, Q.options().dtype(torch::kInt64));
+  const int st = fa_sm75_pack_mask(
+      reinterpret_cast<const uint8_t*>(m.data_ptr<bool>()), own[0], own[1], own[2], nk,
+      own[0] > 1 ? m.stride(0) : 0, own[1] > 1 ? m.stride(1) : 0, own[2] > 1 ? m.stride(2) : 0,
+      m.stride(3), reinterpret_cast<uint64_t*>(bits.data_ptr<int64_t>()),
+      c10::hip::getCurrentHIPStream(Q.device().index()).stream());
+  TORCH_CHECK(st == FA_OK, "attn_mask packing: ", fa_sm75_last_error());
+  p.mask_bits = reinterpret_cast<const uint64_t*>(bits.data_ptr<int64_t>());
+  p.mask_stride_b = own[0] > 1 ? own[1] * own[2] * words : 0;
+  p.mask_stride_h = own[1] > 1 ? own[2] * words : 0;
+  p.mask_stride_q = own[2] > 1 ? words : 0;
+  return bits;
+}
+
 std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_ex(
     torch::Tensor Q, torch::Tensor K, torch::Tensor V, int64_t causal, double scale,
-    bool return_lse) {
+    bool return_lse, c10::optional<torch::Tensor> attn_mask) {
   for (auto* pr : {&Q, &K, &V}) {
     const torch::Tensor& t = *pr;
     TORCH_CHECK(t.is_cuda(), "inputs must be CUDA tensors");
@@ -199,6 +226,8 @@ std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_
   p.o_stride_n = on; p.o_stride_h = eff_stride(O, 1, 0); p.o_stride_b = eff_stride(O, 0, 0);
   p.scale = (float)scale;
   p.causal = (int)causal;
+  torch::Tensor bits;  // lives until the launch is enqueued (stream-ordered reuse)
+  if (attn_mask.has_value()) bits = pack_mask(*attn_mask, Q, K.size(2), p);
   forward_with_workspace(p, Q, "flash_attention_forward_ex");
   return {O, L};
 }
@@ -262,7 +291,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "O (and optionally the fp32 row LSE) for Q [B,Hq,Nq,D], K/V [B,Hkv,Nk,D]; "
         "strided views read in place; causal 0 none, 1 top-left, 2 bottom-right",
         pybind11::arg("Q"), pybind11::arg("K"), pybind11::arg("V"), pybind11::arg("causal"),
-        pybind11::arg("scale"), pybind11::arg("return_lse") = false);
+        pybind11::arg("scale"), pybind11::arg("return_lse") = false,
+        pybind11::arg("attn_mask") = pybind11::none());
   m.def("abi_version", []() { return fa_sm75_abi_version(); });
   m.def("set_kernel_policy", [](int policy) {
     TORCH_CHECK(fa_sm75_set_kernel_policy(policy) == FA_OK,

@@ -81,6 +81,18 @@ int validate(const fa_fwd_params* p, bool fused) {
     return fail(FA_ERR_MISALIGNED, "workspace must be 16-byte aligned");
   if (p->workspace_bytes < 0)
     return fail(FA_ERR_INVALID_ARGUMENT, "workspace_bytes must be non-negative");
+  if (p->mask_bits != nullptr) {
+    if (!fused)
+      return fail(FA_ERR_INVALID_ARGUMENT, "the naive path takes no mask");
+    if ((reinterpret_cast<uintptr_t>(p->mask_bits) & 7u) != 0)
+      return fail(FA_ERR_MISALIGNED, "mask_bits must be 8-byte aligned");
+    if (p->mask_stride_b < 0 || p->mask_stride_h < 0 || p->mask_stride_q < 0)
+      return fail(FA_ERR_INVALID_ARGUMENT, "mask strides must be non-negative");
+    if (p->mask_stride_q != 0 && p->mask_stride_q < (kv_rows(p) + 63) / 64)
+      return fail(FA_ERR_INVALID_ARGUMENT,
+                  "mask row stride %lld is below ceil(seq_len_kv / 64) = %lld words",
+                  (long long)p->mask_stride_q, (long long)((kv_rows(p) + 63) / 64));
+  }
   const int64_t strides[12] = {p->q_stride_b, p->q_stride_h, p->q_stride_n,
                                p->k_stride_b, p->k_stride_h, p->k_stride_n,
                                p->v_stride_b, p->v_stride_h, p->v_stride_n,
@@ -140,6 +152,10 @@ fa::FwdArgs make_args(const fa_fwd_params* p) {
   if (c < 1e-30f) c = 1e-30f;
   a.c = c;
   a.negate_q = p->scale < 0.0f ? 1 : 0;
+  a.mbits = p->mask_bits;
+  a.msb = p->mask_stride_b;
+  a.msh = p->mask_stride_h;
+  a.msq = p->mask_stride_q;
   return a;
 }
 
@@ -220,6 +236,24 @@ int64_t fa_sm75_workspace_size(const fa_fwd_params* p) {
     return 0;
   return fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, INT64_MAX)
       .workspace_bytes;
+}
+
+int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
+                      int64_t cols, int64_t stride_b, int64_t stride_h, int64_t stride_q,
+                      int64_t stride_k, uint64_t* out, void* stream) {
+  g_last_error[0] = '\0';
+  if (batch < 0 || heads < 0 || rows < 0 || cols < 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "mask sizes must be non-negative");
+  if (stride_b < 0 || stride_h < 0 || stride_q < 0 || stride_k < 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "mask strides must be non-negative");
+  if (batch == 0 || heads == 0 || rows == 0 || cols == 0) return FA_OK;
+  if (mask == nullptr || out == nullptr)
+    return fail(FA_ERR_INVALID_ARGUMENT, "mask and out must not be NULL");
+  if ((reinterpret_cast<uintptr_t>(out) & 7u) != 0)
+    return fail(FA_ERR_MISALIGNED, "out must be 8-byte aligned");
+  fa::launch_pack_mask(mask, batch, heads, rows, cols, stride_b, stride_h, stride_q, stride_k,
+                       out, reinterpret_cast<hipStream_t>(stream));
+  return check_launch();
 }
 
 int fa_sm75_set_kernel_policy(int policy) {

@@ -61,7 +61,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool MASK>
 __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d) {
   const FwdArgs& a = d.f;
   using L = DecLds<D>;
@@ -164,6 +164,26 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   _Float16* const my_v0 = v_lds0 + wave * L::Tile;
   _Float16* const my_v1 = v_lds1 + wave * L::Tile;
 
+  // MASK: this lane's mask row read as 32-bit words (word t: keys of 32-key
+  // tile t), through a buffer window over batch b's rows so the load is the
+  // same kind as the K and V loads (their completion order is then the
+  // issue order, which the vmcnt wait below relies on).
+  __amdgpu_buffer_rsrc_t rmask;
+  int m_voff = 0;
+  if (MASK) {
+    const int hq_c = row_ok ? hq : hkv * a.group;
+    const int qi_c = row_ok ? qi : 0;
+    const int64_t words = (NK + 63) / 64;
+    const int64_t span =
+        ((int64_t)(hkv * a.group + a.group - 1) * a.msh + (int64_t)(nq - 1) * a.msq + words) * 8;
+    rmask = make_rsrc(a.mbits + b * a.msb, (int)min(span, (int64_t)INT32_MAX));
+    m_voff = (int)((hq_c * a.msh + qi_c * a.msq) * 8);
+  }
+  auto load_mask = [&](int it, bool valid) -> uint32_t {
+    const int tile = valid ? t_begin + wave + kWaves * it : t_begin;
+    return __builtin_amdgcn_raw_buffer_load_b32(rmask, m_voff + 4 * tile, 0, 0);
+  };
+
   const int v_row = 4 * hi + (gi >> 2);
   const int v_c = 2 * (grp & 1) + ((gi & 3) >> 1);
   const int v_base0 = v_row * L::Pitch + 8 * (v_c ^ hi) + 4 * (gi & 1);
@@ -188,8 +208,10 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   half8 kA[KK], kB[KK];
 
   // One tile: S, softmax, P V.  The loads of the next tile are issued first.
-  auto step = [&](int it, half8 (&kc)[KK], half8 (&kn)[KK], _Float16* vc, _Float16* vn) {
+  auto step = [&](int it, half8 (&kc)[KK], half8 (&kn)[KK], _Float16* vc, _Float16* vn,
+                  uint32_t mw, uint32_t& mw_next) {
     const bool has_next = it + 1 < nt_w;
+    if (MASK) mw_next = load_mask(it + 1, has_next);
     load_k(it + 1, kn, has_next);
     load_v(it + 1, vn, has_next);
     float16v s = (float16v)0.0f;
@@ -198,14 +220,17 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kc[kk], qf[kk], s, 0, 0, 0);
 
     const int kstart = key0 + (wave + kWaves * it) * kDecTile;
-    const bool need_mask =
-        (kstart + kDecTile > NK) || (CAUSAL && kstart + kDecTile - 1 > a.diag);
+    bool need_mask = (kstart + kDecTile > NK) || (CAUSAL && kstart + kDecTile - 1 > a.diag);
+    if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
     if (need_mask) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      const uint32_t mws = mw >> (4 * hi);  // bit 8 (i / 4) + i % 4: element i
+      static_for<16>([&](auto i_c) {
+        constexpr int i = decltype(i_c)::value;
         const int key = kstart + 8 * (i >> 2) + 4 * hi + (i & 3);
-        if (key >= NK || (CAUSAL && key > diag_row)) s[i] = -__builtin_inff();
-      }
+        bool masked = key >= NK || (CAUSAL && key > diag_row);
+        if (MASK) masked = masked || ((mws >> (8 * (i >> 2) + (i & 3))) & 1) == 0;
+        if (masked) s[i] = -__builtin_inff();
+      });
     }
     float mx = s[0];
 #pragma unroll
@@ -235,7 +260,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     }
     // V of this tile has landed once only the next tile's loads are pending
     // (loads complete in order).
-    wait_vmcnt<KK + SEGS>();
+    wait_vmcnt<KK + SEGS + (MASK ? 1 : 0)>();
     half8 vf[NPV];
 #pragma unroll
     for (int v = 0; v < NPV; ++v) vf[v] = read_v(vc, v);
@@ -247,14 +272,16 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   };
 
   if (nt_w > 0) {
+    uint32_t mwA = ~0u, mwB = ~0u;
+    if (MASK) mwA = load_mask(0, true);
     load_k(0, kA, true);
     load_v(0, my_v0, true);
     int it = 0;
     for (; it + 1 < nt_w; it += 2) {
-      step(it, kA, kB, my_v0, my_v1);
-      step(it + 1, kB, kA, my_v1, my_v0);
+      step(it, kA, kB, my_v0, my_v1, mwA, mwB);
+      step(it + 1, kB, kA, my_v1, my_v0, mwB, mwA);
     }
-    if (it < nt_w) step(it, kA, kB, my_v0, my_v1);
+    if (it < nt_w) step(it, kA, kB, my_v0, my_v1, mwA, mwB);
   }
 
   // ---- merge the four waves through LDS (the V tiles are free now) --------
@@ -459,12 +486,16 @@ int launch_decode_forward(const FwdArgs& a, const DecodePlan& pl, int head_dim, 
                   ? d.part_o + (int64_t)pl.units * pl.splits * pl.rows * head_dim
                   : nullptr;
   const dim3 grid((unsigned)((int64_t)pl.units * pl.splits));
-#define FA_DEC(DD, C) hipLaunchKernelGGL((fa_decode_kernel<DD, C>), grid, dim3(kThreads), 0, stream, d)
+#define FA_DEC(DD, C, M) \
+  hipLaunchKernelGGL((fa_decode_kernel<DD, C, M>), grid, dim3(kThreads), 0, stream, d)
+#define FA_DEC_M(DD, C) \
+  if (a.mbits != nullptr) FA_DEC(DD, C, true); else FA_DEC(DD, C, false)
   if (head_dim == 128) {
-    if (causal) FA_DEC(128, true); else FA_DEC(128, false);
+    if (causal) { FA_DEC_M(128, true); } else { FA_DEC_M(128, false); }
   } else {
-    if (causal) FA_DEC(64, true); else FA_DEC(64, false);
+    if (causal) { FA_DEC_M(64, true); } else { FA_DEC_M(64, false); }
   }
+#undef FA_DEC_M
 #undef FA_DEC
   if (pl.splits > 1) {
     const dim3 cgrid((unsigned)((int64_t)pl.units * pl.rows));

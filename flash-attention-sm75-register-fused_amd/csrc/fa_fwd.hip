@@ -64,8 +64,9 @@ namespace {
 //     end of step j+1 to land; every K/V tile serves 256 query rows, and each
 //     wave issues half as many direct loads (waves 0-3 load K, 4-7 load V).
 // KV_SAME_STRIDE: K and V rows have the same stride, so the direct-load
-// offsets are shared (saves registers).
-template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES>
+// offsets are shared (saves registers).  MASK: an explicit mask (one 64-bit
+// word per query row and tile, loaded a step ahead) hides keys too.
+template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, bool MASK>
 __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
   using L = Lds<D>;
   constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
@@ -115,6 +116,9 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   const int NK = a.nk;  // key rows
 
   const _Float16* Qp = a.q + b * a.qsb + hq * a.qsh;
+  // Mask bits of this lane's query row (rows past N read row N - 1).
+  const uint64_t* mrow =
+      MASK ? a.mbits + b * a.msb + hq * a.msh + (int64_t)min(qrow, N - 1) * a.msq : nullptr;
   const _Float16* Kp = a.k + b * a.ksb + hkv * a.ksh;
   const _Float16* Vp = a.v + b * a.vsb + hkv * a.vsh;
 
@@ -243,23 +247,28 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   float mc = 0.0f;  // running max of tile j's rows, times c2 (exp2 offset)
 
   // Prepares tile j's scores for its softmax: masks them if tile j crosses
-  // the sequence end or this wave's causal diagonal (the unmasked row max mx
-  // is then recomputed), raises the running max when some row outgrew it by
-  // more than 2^kRescaleLog2 (rescaling O and l), and sets mc.
-  auto prepare = [&](int j, float16v (&s)[2], float mx) {
+  // the sequence end or this wave's causal diagonal, or (MASK) hides a key
+  // from some row of the wave (the unmasked row max mx is then recomputed),
+  // raises the running max when some row outgrew it by more than
+  // 2^kRescaleLog2 (rescaling O and l), and sets mc.  mw: the lane's mask
+  // word of tile j (bit k: key 64 j + k visible).
+  auto prepare = [&](int j, float16v (&s)[2], float mx, uint64_t mw) {
     const int kstart = j * kBlockN;
-    const bool need_mask =
+    bool need_mask =
         (kstart + kBlockN > NK) || (CAUSAL && kstart + kBlockN - 1 > qw + a.diag);
+    if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
     if (need_mask) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
-          const bool masked = (key >= NK) || (CAUSAL && key > qrow + a.diag);
-          if (masked) s[t][i] = -__builtin_inff();
-        }
-      }
+      const uint64_t mws = mw >> (4 * hi);  // bit 32 t + 8 (i / 4) + i % 4: element (t, i)
+      // static_for: a loop the unroller leaves rolled would index s at run
+      // time and move the score registers to scratch memory.
+      static_for<32>([&](auto e_c) {
+        constexpr int e = decltype(e_c)::value;
+        constexpr int t = e >> 4, i = e & 15;
+        const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
+        bool masked = (key >= NK) || (CAUSAL && key > qrow + a.diag);
+        if (MASK) masked = masked || ((mws >> (32 * t + 8 * (i >> 2) + (i & 3))) & 1) == 0;
+        if (masked) s[t][i] = -__builtin_inff();
+      });
       mx = halves_max(row_max(s));
     }
     const bool grow = (mx - m_run) * c2 > kRescaleLog2;
@@ -295,9 +304,11 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // each of the first MFMAs, so the address unit's queueing overlaps MFMA
     // execution.  Past the last tile the windows are empty.
     __amdgpu_buffer_rsrc_t rk_next, rv_next;
+    uint64_t mw_next = ~0ull;
     if (HAS_NEXT) {
       rk_next = k_window(j + STAGES);
       rv_next = v_window(j + STAGES - 1);
+      if (MASK) mw_next = mrow[j + 1];  // consumed by prepare(j + 1) at the end
     }
     _Float16* k_dst = kbuf(std::integral_constant<int, U>{});
     _Float16* v_dst = vbuf(std::integral_constant<int, U + STAGES - 1>{});
@@ -395,7 +406,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     });
 
     if (HAS_NEXT) {
-      prepare(j + 1, s_nxt, mx_next);
+      prepare(j + 1, s_nxt, mx_next, mw_next);
       // The loads of the previous step have landed (those of this step may
       // still be in flight with three stages), and every wave is done with
       // the buffers the next step's loads overwrite.
@@ -422,7 +433,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         s_buf[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(k_lds0, t * KK + kk), qf[kk],
                                                              s_buf[0][t], 0, 0, 0);
     }
-    prepare(0, s_buf[0], halves_max(row_max(s_buf[0])));
+    prepare(0, s_buf[0], halves_max(row_max(s_buf[0])), MASK ? mrow[0] : ~0ull);
     // Step 0 loads K_STAGES into K_0's buffer: every wave must be done
     // reading it for S_0 first.
     __syncthreads();
@@ -481,14 +492,14 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
 
 namespace {
 
-template <int WAVES>
+template <int WAVES, bool MASK>
 void launch_waves(const FwdArgs& a, int batch, int head_dim, bool causal, hipStream_t stream) {
   const bool same = a.ksn == a.vsn;
   FwdArgs args = a;
   const dim3 grid((unsigned)plan_grid(args, batch, 32 * WAVES));
   const dim3 block(64 * WAVES);
 #define FA_LAUNCH(D, C, S) \
-  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES>), grid, block, 0, stream, args)
+  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK>), grid, block, 0, stream, args)
   if (head_dim == 128) {
     if (causal) {
       if (same) FA_LAUNCH(128, true, true); else FA_LAUNCH(128, true, false);
@@ -511,12 +522,15 @@ void launch_waves(const FwdArgs& a, int batch, int head_dim, bool causal, hipStr
 // for (FA_POLICY_WIDE): measured on C4 it is ~4% slower than the 4-wave
 // kernel -- with one workgroup per CU both waves of a SIMD stop at the same
 // barrier, where two independent 4-wave workgroups cover each other's.
+// Masked calls always take the 4-wave kernel.
 int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
                          int policy, hipStream_t stream) {
-  if (policy == 2)
-    launch_waves<8>(a, batch, head_dim, causal, stream);
+  if (a.mbits != nullptr)
+    launch_waves<4, true>(a, batch, head_dim, causal, stream);
+  else if (policy == 2)
+    launch_waves<8, false>(a, batch, head_dim, causal, stream);
   else
-    launch_waves<4>(a, batch, head_dim, causal, stream);
+    launch_waves<4, false>(a, batch, head_dim, causal, stream);
   return 0;
 }
 

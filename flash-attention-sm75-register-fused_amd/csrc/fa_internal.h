@@ -31,6 +31,8 @@ struct FwdArgs {
   int xcds;         // 8: units split evenly over the XCDs, else 1 (launcher)
   float c;          // |scale| * log2(e), clamped away from 0
   int negate_q;     // scale < 0: Q fragments are negated (exact in fp16)
+  const uint64_t* mbits;   // explicit mask bits or nullptr (see fa_fwd_params)
+  int64_t msb, msh, msq;   // its strides in 64-bit words
 };
 
 // Launches the fused MFMA kernel; all arguments already validated.
@@ -62,6 +64,11 @@ DecodePlan plan_decode(const FwdArgs& a, int batch, int head_dim, bool causal,
                        int64_t workspace_bytes);
 int launch_decode_forward(const FwdArgs& a, const DecodePlan& plan, int head_dim, bool causal,
                           void* workspace, hipStream_t stream);
+
+// Boolean mask -> bit rows (fa_mask.hip).
+int launch_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
+                     int64_t cols, int64_t sb, int64_t sh, int64_t sq, int64_t sk,
+                     uint64_t* out, hipStream_t stream);
 
 // Three-kernel path through an fp32 [B*Hq, N, N] score workspace.
 int launch_naive_forward(const FwdArgs& a, int batch, int head_dim, bool causal,

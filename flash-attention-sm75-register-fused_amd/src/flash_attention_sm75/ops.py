@@ -111,7 +111,8 @@ def flash_attention_forward_lse(Q, K, V, causal=False, scale=None):
 _CAUSAL_CODES = {False: 0, True: 1, "top_left": 1, "bottom_right": 2}
 
 
-def flash_attention_forward_ex(Q, K, V, causal=False, scale=None, return_lse=False):
+def flash_attention_forward_ex(Q, K, V, causal=False, scale=None, return_lse=False,
+                               attn_mask=None):
     """Forward over separate query/key lengths and strided views.
 
     No reference counterpart: the reference binding requires Nq == Nk and
@@ -128,6 +129,9 @@ def flash_attention_forward_ex(Q, K, V, causal=False, scale=None, return_lse=Fal
             j <= i + N_k - N_q).  A query that sees no key gets a zero row.
         scale: softmax scale (default 1/sqrt(D)).
         return_lse: also return the fp32 natural-log row LSE [B, H_q, N_q].
+        attn_mask: optional bool tensor broadcastable to [B, H_q, N_q, N_k],
+            True = the key takes part (torch SDPA's boolean attn_mask); it is
+            packed to bits on the GPU and combines with ``causal``.
 
     Returns:
         O [B, H_q, N_q, D] float16 with Q's memory layout when Q is dense,
@@ -143,5 +147,6 @@ def flash_attention_forward_ex(Q, K, V, causal=False, scale=None, return_lse=Fal
             f"causal must be False, True, 'top_left' or 'bottom_right', got {causal!r}"
         ) from None
     _check_gqa_heads(Q, K)
-    o, lse = _C.flash_attention_forward_ex(Q, K, V, code, float(scale), bool(return_lse))
+    o, lse = _C.flash_attention_forward_ex(Q, K, V, code, float(scale), bool(return_lse),
+                                           attn_mask)
     return (o, lse) if return_lse else o

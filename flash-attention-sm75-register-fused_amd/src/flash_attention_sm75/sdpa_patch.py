@@ -9,9 +9,11 @@ attention through the gfx950 kernel.
 
 Differences from the reference, all of which widen what runs on the kernel
 without changing results:
-  * calls with ``N_q != N_k`` (KV-cache decode and chunked prefill without a
-    mask) use the kernel instead of falling back; ``is_causal`` keeps SDPA's
-    top-left alignment (key j visible to query i iff j <= i);
+  * calls with ``N_q != N_k`` (KV-cache decode, chunked prefill) use the
+    kernel instead of falling back; ``is_causal`` keeps SDPA's top-left
+    alignment (key j visible to query i iff j <= i);
+  * boolean ``attn_mask`` (what transformers builds for padded batches) runs
+    on the kernel too; additive float masks fall back;
   * Q/K/V views are read in place (transformers passes [B, N, H, D] buffers
     viewed as [B, H, N, D]) and O keeps Q's layout, so the caller's
     ``transpose(1, 2).contiguous()`` is free;
@@ -39,7 +41,7 @@ def _record_fallback(reason: str):
     _stats["fallback_reasons"][reason] = _stats["fallback_reasons"].get(reason, 0) + 1
 
 
-def _fallback_reason(query, key, value, attn_mask, dropout_p, kwargs):
+def _fallback_reason(query, key, value, attn_mask, dropout_p, is_causal, kwargs):
     """Why a call cannot run on the kernel, or None (reference :47-64)."""
     if not query.is_cuda:
         return "not_cuda"
@@ -53,8 +55,10 @@ def _fallback_reason(query, key, value, attn_mask, dropout_p, kwargs):
         return "kv_shape_mismatch"
     if dropout_p != 0.0:
         return "dropout"
-    if attn_mask is not None:
-        return "has_attn_mask"
+    if attn_mask is not None and attn_mask.dtype != torch.bool:
+        return "has_attn_mask"  # additive float masks stay with torch
+    if attn_mask is not None and is_causal:
+        return "mask_and_causal"  # torch rejects the combination; let it say so
     if key.size(0) != query.size(0):
         return "batch_mismatch"
     if key.size(1) == 0 or query.size(1) % key.size(1) != 0:
@@ -72,14 +76,15 @@ def _fallback_reason(query, key, value, attn_mask, dropout_p, kwargs):
 def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
                   scale=None, **kwargs):
     _stats["total"] += 1
-    reason = _fallback_reason(query, key, value, attn_mask, dropout_p, kwargs)
+    reason = _fallback_reason(query, key, value, attn_mask, dropout_p, is_causal, kwargs)
     if reason is not None:
         _record_fallback(reason)
         # everything passes through unchanged
         return _original_sdpa(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
                               is_causal=is_causal, scale=scale, **kwargs)
     _stats["flash"] += 1
-    return flash_attention_forward_ex(query, key, value, causal=bool(is_causal), scale=scale)
+    return flash_attention_forward_ex(query, key, value, causal=bool(is_causal), scale=scale,
+                                      attn_mask=attn_mask)
 
 
 def apply_patch():

@@ -85,6 +85,14 @@ typedef struct fa_fwd_params {
   int64_t workspace_bytes; /* its size; fa_sm75_workspace_size() gives the
                          amount for full parallelism.  With less, the call
                          still runs, on fewer workgroups, and allocates nothing */
+  /* Optional explicit mask (torch SDPA's boolean attn_mask), or NULL: bit k
+   * of word w of row (b, h, i) set <=> key 64w + k is visible to query i of
+   * query head h in batch b; fa_sm75_pack_mask builds it.  Strides are in
+   * 64-bit words (0 broadcasts a dimension); a nonzero row stride must be
+   * at least ceil(seq_len_kv / 64) words.  Combines (AND) with `causal`.  A row that
+   * sees no key gets O = 0 and LSE = -inf. */
+  const uint64_t* mask_bits;
+  int64_t mask_stride_b, mask_stride_h, mask_stride_q;
 } fa_fwd_params;
 
 /* Fills strides for contiguous [B,H,N,D] Q/O and [B,Hkv,Nk,D] K/V tensors. */
@@ -102,6 +110,15 @@ int fa_sm75_forward(const fa_fwd_params* p);
  * for invalid parameters, which fa_sm75_forward reports.  No reference
  * counterpart (the reference has no decode path). */
 int64_t fa_sm75_workspace_size(const fa_fwd_params* p);
+
+/* Packs a boolean mask (one byte per element, nonzero = visible) of shape
+ * [batch, heads, rows, cols] with element strides (any, 0 included) into the
+ * bit layout of fa_fwd_params.mask_bits: out is [batch, heads, rows, words]
+ * contiguous, words = ceil(cols / 64), bits past cols clear.  Asynchronous
+ * on `stream`.  No reference counterpart (the reference takes no mask). */
+int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
+                      int64_t cols, int64_t stride_b, int64_t stride_h, int64_t stride_q,
+                      int64_t stride_k, uint64_t* out, void* stream);
 
 /* Three-pass reference-style path (QK^T -> row softmax -> PV) through an fp32
  * score workspace of batch*heads_q*seq_len*seq_len floats.  Replaces reference

@@ -56,6 +56,14 @@ def causal_mask(nq: int, nk: int, causal, row0: int = 0, rows: int | None = None
     return cols > rws + diag
 
 
+def visible(attn_mask, shape):
+    """Explicit boolean mask (True = the key takes part, torch SDPA's boolean
+    attn_mask; no reference counterpart) broadcast to ``shape``, or None."""
+    if attn_mask is None:
+        return None
+    return np.broadcast_to(np.asarray(attn_mask, dtype=bool), shape)
+
+
 def _softmax_rows_f32(S: np.ndarray) -> np.ndarray:
     """torch.softmax(S, dim=-1) in fp32: exp(S - rowmax) / rowsum.
 
@@ -69,7 +77,7 @@ def _softmax_rows_f32(S: np.ndarray) -> np.ndarray:
     return E / np.where(tot > 0, tot, np.float32(1))
 
 
-def attention_reference(Q, K, V, causal=False, scale=None, return_f32=False):
+def attention_reference(Q, K, V, causal=False, scale=None, return_f32=False, attn_mask=None):
     """The reference's math path, restated (attention_ref.py:10-45).
 
     fp16 [B,H,N,D] inputs -> fp32 upcast (:28-30) -> S = Q K^T * scale (:32)
@@ -90,13 +98,16 @@ def attention_reference(Q, K, V, causal=False, scale=None, return_f32=False):
     mask = causal_mask(Q.shape[-2], K.shape[-2], causal)
     if mask is not None:
         S[..., mask] = -np.inf
+    vis = visible(attn_mask, S.shape)
+    if vis is not None:
+        S[~vis] = -np.inf
     P = _softmax_rows_f32(S)
     O = np.matmul(P, vf)
     return O if return_f32 else O.astype(np.float16)
 
 
 def attention_reference_chunked(Q, K, V, causal=False, scale=None, rows=512,
-                                heads=None, return_f32=False):
+                                heads=None, return_f32=False, attn_mask=None):
     """Same math as :func:`attention_reference`, one (b, h, row block) at a time.
 
     Rows of the softmax are independent, so evaluating [rows, N] blocks of S
@@ -120,6 +131,7 @@ def attention_reference_chunked(Q, K, V, causal=False, scale=None, rows=512,
     hs = list(range(Hq)) if heads is None else list(heads)
     out = np.empty((B, len(hs), N, D), dtype=np.float32 if return_f32 else np.float16)
     sc = np.float32(scale)
+    vis = visible(attn_mask, (B, Hq, N, Nk))
     for b in range(B):
         for oi, h in enumerate(hs):
             kf = K[b, h // group].astype(np.float32)
@@ -132,13 +144,15 @@ def attention_reference_chunked(Q, K, V, causal=False, scale=None, rows=512,
                 mask = causal_mask(N, Nk, causal, r0, r1 - r0)
                 if mask is not None:
                     S[mask] = -np.inf
+                if vis is not None:
+                    S[~vis[b, h, r0:r1]] = -np.inf
                 P = _softmax_rows_f32(S)
                 o = P @ vf
                 out[b, oi, r0:r1] = o if return_f32 else o.astype(np.float16)
     return out
 
 
-def attention_lse(Q, K, causal=False, scale=None, dtype=np.float64):
+def attention_lse(Q, K, causal=False, scale=None, dtype=np.float64, attn_mask=None):
     """Row log-sum-exp: LSE_i = log sum_{j visible} exp(scale * q_i . k_j).
 
     No reference counterpart (the reference names LSE only as future work);
@@ -151,6 +165,7 @@ def attention_lse(Q, K, causal=False, scale=None, dtype=np.float64):
     if scale is None:
         scale = default_scale(D)
     out = np.empty((B, Hq, N), dtype=dtype)
+    vis = visible(attn_mask, (B, Hq, N, K.shape[2]))
     for b in range(B):
         for h in range(Hq):
             q = Q[b, h].astype(dtype)
@@ -159,6 +174,8 @@ def attention_lse(Q, K, causal=False, scale=None, dtype=np.float64):
             mask = causal_mask(N, K.shape[2], causal)
             if mask is not None:
                 S[mask] = -np.inf
+            if vis is not None:
+                S[~vis[b, h]] = -np.inf
             m = S.max(axis=-1, keepdims=True)
             m = np.where(np.isfinite(m), m, 0)
             with np.errstate(divide="ignore"):
@@ -166,7 +183,7 @@ def attention_lse(Q, K, causal=False, scale=None, dtype=np.float64):
     return out
 
 
-def attention_f64(Q, K, V, causal=False, scale=None):
+def attention_f64(Q, K, V, causal=False, scale=None, attn_mask=None):
     """Brute-force float64 attention (two-pass softmax), for pinning the fp32 path."""
     Q = np.asarray(Q)
     K, V = expand_kv_for_gqa(Q, np.asarray(K), np.asarray(V))
@@ -179,6 +196,9 @@ def attention_f64(Q, K, V, causal=False, scale=None):
     mask = causal_mask(Q.shape[-2], K.shape[-2], causal)
     if mask is not None:
         S[..., mask] = -np.inf
+    vis = visible(attn_mask, S.shape)
+    if vis is not None:
+        S[~vis] = -np.inf
     m = S.max(axis=-1, keepdims=True)
     m = np.where(np.isfinite(m), m, 0.0)
     E = np.exp(S - m)

@@ -49,7 +49,7 @@ def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("fa_sm75_forward", "fa_sm75_naive_forward", "fa_sm75_last_error",
               "fa_sm75_status_string", "fa_sm75_abi_version", "fa_sm75_set_contiguous_strides",
-              "fa_sm75_workspace_size",
+              "fa_sm75_workspace_size", "fa_sm75_pack_mask",
               "launch_flash_attention_forward", "launch_flash_attention_forward_scalar",
               "launch_flash_attention_forward_wmma_qk", "launch_naive_attention"):
         assert n in names, n
@@ -155,6 +155,33 @@ def test_workspace_size(lib):
         assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == 0
     finally:
         lib.fa_sm75_set_kernel_policy(0)
+
+
+def test_pack_mask_validation(lib):
+    f = lib.fa_sm75_pack_mask
+    f.argtypes = [ctypes.c_void_p] + [ctypes.c_int64] * 8 + [ctypes.c_void_p, ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    assert f(0x1000, 1, 1, 1, 0, 0, 0, 0, 1, 0x1000, None) == 0      # empty: no-op
+    assert f(0x1000, -1, 1, 1, 8, 0, 0, 0, 1, 0x1000, None) == 1
+    assert b"non-negative" in lib.fa_sm75_last_error()
+    assert f(0x1000, 1, 1, 1, 8, 0, 0, -1, 1, 0x1000, None) == 1
+    assert f(0, 1, 1, 1, 8, 0, 0, 0, 1, 0x1000, None) == 1
+    assert f(0x1000, 1, 1, 1, 8, 0, 0, 0, 1, 0x1004, None) == 4
+    assert b"8-byte aligned" in lib.fa_sm75_last_error()
+
+
+def test_mask_param_validation(lib):
+    p = make(lib, mask_bits=0x1004)
+    assert lib.fa_sm75_forward(ctypes.byref(p)) == 4
+    p = make(lib, mask_bits=0x1000, mask_stride_q=-1)
+    assert lib.fa_sm75_forward(ctypes.byref(p)) == 1
+    p = make(lib, mask_bits=0x1000, mask_stride_q=1, seq_len_kv=200)  # 200 keys need 4 words
+    lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+    assert lib.fa_sm75_forward(ctypes.byref(p)) == 1
+    assert b"below ceil(seq_len_kv / 64)" in lib.fa_sm75_last_error()
+    p = make(lib, mask_bits=0x1000)
+    assert lib.fa_sm75_naive_forward(ctypes.byref(p), ctypes.c_void_p(0x1000)) == 1
+    assert b"naive path takes no mask" in lib.fa_sm75_last_error()
 
 
 def test_abi_version(lib):

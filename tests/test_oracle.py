@@ -325,3 +325,59 @@ def test_rows_without_visible_keys_are_zero():
     # row 30 sees key 0 only
     np.testing.assert_allclose(o[0, 0, 30], v[0, 0, 0].astype(np.float32), atol=0)
     np.testing.assert_allclose(ref.attention_f64(q, k, v, causal=2)[0, 0, :30], 0)
+
+
+# ---- explicit boolean attn_mask (no reference counterpart; torch SDPA's
+# semantics, pinned against torch's CPU implementation) -----------------------
+
+@pytest.mark.parametrize("mshape", [(2, 4, 9, 30), (2, 1, 9, 30), (9, 30), (2, 1, 1, 30)])
+def test_bool_mask_matches_torch_sdpa_cpu(mshape):
+    import torch
+    q = rnd((2, 4, 9, 64), 50)
+    k = rnd((2, 2, 30, 64), 51)
+    v = rnd((2, 2, 30, 64), 52)
+    r = np.random.default_rng(53)
+    mask = r.random(mshape) < 0.7
+    mask[..., 0] = True  # every row sees a key: torch gives NaN for empty rows
+    got = ref.attention_reference(q, k, v, attn_mask=mask, return_f32=True)
+    ke, ve = ref.expand_kv_for_gqa(q, k, v)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q).float(), torch.from_numpy(ke).float(), torch.from_numpy(ve).float(),
+        attn_mask=torch.from_numpy(np.ascontiguousarray(mask))).numpy()
+    np.testing.assert_allclose(got, want, atol=2e-6)
+    np.testing.assert_allclose(ref.attention_f64(q, k, v, attn_mask=mask), got, atol=2e-5)
+    chunk = ref.attention_reference_chunked(q, k, v, attn_mask=mask, rows=4, return_f32=True)
+    np.testing.assert_allclose(chunk, got, atol=1e-6)
+    # LSE: closed form over the visible keys only
+    lse = ref.attention_lse(q, k, attn_mask=mask)
+    full = np.broadcast_to(mask, (2, 4, 9, 30))
+    S = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), ke.astype(np.float64)) / 8.0
+    want_lse = np.log(np.where(full, np.exp(S), 0).sum(-1))
+    np.testing.assert_allclose(lse, want_lse, atol=1e-10)
+
+
+def test_bool_mask_special_cases():
+    q = rnd((1, 2, 12, 64), 54)
+    k = rnd((1, 2, 12, 64), 55)
+    v = rnd((1, 2, 12, 64), 56)
+    plain = ref.attention_reference(q, k, v, return_f32=True)
+    ones = np.ones((12, 12), bool)
+    np.testing.assert_array_equal(ref.attention_reference(q, k, v, attn_mask=ones, return_f32=True),
+                                  plain)
+    tril = np.tril(ones)
+    np.testing.assert_allclose(ref.attention_reference(q, k, v, attn_mask=tril, return_f32=True),
+                               ref.attention_reference(q, k, v, causal=True, return_f32=True),
+                               atol=0)
+    # a row with no visible key gives 0 (the kernels' 1/l -> 0 rule), not NaN
+    m = ones.copy()
+    m[3] = False
+    o = ref.attention_reference(q, k, v, attn_mask=m, return_f32=True)
+    assert np.all(o[:, :, 3] == 0) and np.all(np.isfinite(o))
+    assert np.all(np.isneginf(ref.attention_lse(q, k, attn_mask=m)[:, :, 3]))
+    # mask combined with causal: AND of the two
+    r = np.random.default_rng(57).random((12, 12)) < 0.5
+    np.testing.assert_allclose(
+        ref.attention_reference(q, k, v, causal=True, attn_mask=r | np.eye(12, dtype=bool),
+                                return_f32=True),
+        ref.attention_reference(q, k, v, attn_mask=(r | np.eye(12, dtype=bool)) & tril,
+                                return_f32=True), atol=0)
