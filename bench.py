@@ -283,6 +283,8 @@ def main():
     ap.add_argument("--all", action="store_true", help="also time C1..C5 (stderr)")
     ap.add_argument("--decode", action="store_true",
                     help="also time the split-K decode workloads D1..D3 (stderr)")
+    ap.add_argument("--decode-only", choices=sorted(DECODE_CONFIGS), default=None,
+                    help="profiling aid: time only this decode workload (stderr), no JSON line")
     ap.add_argument("--hf", action="store_true",
                     help="also time a random-init Qwen2-0.5B-shaped model, unpatched vs "
                          "patched SDPA (stderr)")
@@ -328,6 +330,11 @@ def main():
             med = km[len(km) // 2]
             log(f"[{c}] {DESCR[c]}: median kernel {med:.4f} ms -> "
                 f"{flops(b_, hq_, n_, d_, ca_) / med / 1e9:.1f} TFLOPS")
+
+    if args.decode_only:  # profiling aid: one decode workload, nothing else
+        ms, gbs = time_decode(args.decode_only, steps=args.steps, warmup=args.warmup)
+        log(f"[{args.decode_only}] split-K {ms:.4f} ms -> {gbs:.0f} GB/s")
+        return
 
     if args.decode:
         for c in sorted(DECODE_CONFIGS):
