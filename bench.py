@@ -121,9 +121,11 @@ def time_gpu(cfg, steps, warmup, data="randn"):
     return wall, kern_ms
 
 
-def cpu_baseline(cfg, budget_s=20.0):
-    """Reference math path (torch on the host CPU) on a bounded sample:
-    whole query heads of the workload, as many as fit in ``budget_s``."""
+def cpu_baseline(cfg, budget_s=20.0, min_s=10.0):
+    """Reference math path (torch on the host CPU) on a bounded sample: whole
+    (batch, query-head) slices of the workload in order, stopping at
+    ``budget_s``, or once every slice ran and at least ``min_s`` passed (the
+    slices are then repeated, so a fast host still times ~10 s of work)."""
     import torch
 
     from oracle import attention_ref as ref
@@ -132,15 +134,14 @@ def cpu_baseline(cfg, budget_s=20.0):
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
     q, k, v = make_inputs(cfg)
-    done, t_used, b = 0, 0.0, 0
-    heads = []
-    while t_used < budget_s and done < B * Hq:
-        b, h = divmod(done, Hq)
+    done, t_used = 0, 0.0
+    total = B * Hq
+    while t_used < budget_s and not (done >= total and t_used >= min_s):
+        b, h = divmod(done % total, Hq)
         t0 = time.perf_counter()
         ref.attention_reference_torch_cpu(q[b:b + 1], k[b:b + 1], v[b:b + 1], causal=causal,
                                           heads=[h])
         t_used += time.perf_counter() - t0
-        heads.append((b, h))
         done += 1
     f = flops(1, done, N, D, causal)
     return {
@@ -148,9 +149,10 @@ def cpu_baseline(cfg, budget_s=20.0):
         "unit": "TFLOPS",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{done} of {B * Hq} (batch, query-head) slices of {cfg}, all {N} rows each, "
-                   f"{t_used:.1f} s; torch CPU restatement of reference "
-                   f"src/reference/attention_ref.py (fp32, full NxN scores then causal mask)"),
+        "sample": (f"{done} (batch, query-head) slices of {cfg} ({total} per workload, "
+                   f"{done / total:.2f} workloads), all {N} rows each, {t_used:.1f} s; torch CPU "
+                   f"restatement of reference src/reference/attention_ref.py (fp32, full NxN "
+                   f"scores then causal mask)"),
     }
 
 
