@@ -37,7 +37,7 @@ namespace {
 
 constexpr int kDecTile = 32;       // keys per wave tile
 constexpr int kDecMinTiles = 8;    // fewest tiles a split is given
-constexpr int kDecTargetWgs = 512; // two workgroups per CU
+constexpr int kDecTargetWgs = 256; // one workgroup per CU (measured best)
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
