@@ -19,6 +19,9 @@ Printed: ONE JSON line on stdout (rank 0).  Besides the driver's keys it holds
                 launch, on the launch stream) against the MFMA peak; traffic
                 is the HBM bytes per launch from the committed rocprofv3
                 FETCH_SIZE/WRITE_SIZE summary for this workload, when present;
+                sustained_mfma is a dense fp16 GEMM (hipBLASLt) on random
+                operands timed in the same run, the rate the MFMA pipes hold
+                under the board's power limit, and the kernel's share of it;
   cpu_baseline  the reference math path (restated with torch on the host
                 CPU) timed on a bounded sample of the same workload.
 Diagnostics go to stderr.
@@ -119,6 +122,35 @@ def time_gpu(cfg, steps, warmup, data="randn"):
     wall = time.perf_counter() - t0
     kern_ms = sorted(a.elapsed_time(b) for a, b in ev)
     return wall, kern_ms
+
+
+def gemm_ceiling(m=16384, steps=5, warmup=2):
+    """Dense fp16 GEMM (torch.matmul -> hipBLASLt) on N(0,1) data, m^3, timed
+    with HIP events on the same GPU in the same run: what the MFMA pipes
+    sustain on random fp16 operands under this board's power limit, against
+    which the attention kernel's own MFMA-bound rate is read (the 2.5 PFLOP/s
+    dense peak assumes the 2.4 GHz peak clock)."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator("cpu").manual_seed(11)
+    a = torch.randn(m, m, generator=g).half().to(dev)
+    b = torch.randn(m, m, generator=g).half().to(dev)
+    c = torch.empty(m, m, dtype=torch.float16, device=dev)
+    for _ in range(warmup):
+        torch.matmul(a, b, out=c)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    torch.cuda.synchronize()
+    for s, e in ev:
+        s.record()
+        torch.matmul(a, b, out=c)
+        e.record()
+    torch.cuda.synchronize()
+    ms = sorted(s.elapsed_time(e) for s, e in ev)[steps // 2]
+    del a, b, c
+    torch.cuda.empty_cache()
+    return 2.0 * m ** 3 / (ms * 1e-3) / 1e12
 
 
 def cpu_baseline(cfg, budget_s=20.0, min_s=10.0):
@@ -281,6 +313,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-gemm-ceiling", action="store_true",
+                    help="skip the fp16 GEMM run that measures the sustained MFMA rate")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--all", action="store_true", help="also time C1..C5 (stderr)")
     ap.add_argument("--decode", action="store_true",
@@ -366,6 +400,16 @@ def main():
         f"(median {kern_ms[len(kern_ms) // 2]:.4f}, min {kern_ms[0]:.4f}) -> "
         f"{value:.1f} TFLOPS wall, {achieved:.1f} TFLOPS kernel")
 
+    ceiling = None
+    if not args.no_gemm_ceiling:
+        gemm = gemm_ceiling()
+        ceiling = {
+            "gemm_tflops": round(gemm, 1),
+            "gemm": "torch.matmul fp16 16384x16384x16384 (hipBLASLt), N(0,1) operands, same run",
+            "kernel_vs_gemm": round(achieved / gemm, 4),
+        }
+        log(f"[gemm-ceiling] {ceiling}")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.cpu_budget)
@@ -401,6 +445,7 @@ def main():
             "traffic": traffic,
             "algorithmic_bytes": min_bytes(B, Hq, Hkv, N, D),
             "kernel_avg_ms": round(avg_kernel_ms, 5),
+            "sustained_mfma": ceiling,
         },
         "cpu_baseline": cpu,
     }

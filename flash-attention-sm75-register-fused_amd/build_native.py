@@ -15,9 +15,12 @@ what the repository's build check expects.
 from __future__ import annotations
 
 import os
+import shutil
 import subprocess
 import sys
 import sysconfig
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
@@ -29,16 +32,25 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIP_LIB_NAME = "libflash_attn_sm75_hip.so"
 EXT_NAME = "flash_attn_sm75_cuda"
 
-HIP_SOURCES = ["fa_fwd.hip", "fa_decode.hip", "fa_mask.hip", "fa_naive.hip", "fa_capi.hip"]
+# The fused kernel's instances (fa_fwd_d*.hip) are separate translation units
+# so that they compile in parallel.
+HIP_SOURCES = [
+    "fa_fwd_d128.hip", "fa_fwd_d128_mask.hip", "fa_fwd_d128_w8.hip",
+    "fa_fwd_d64.hip", "fa_fwd_d64_mask.hip", "fa_fwd_d64_w8.hip",
+    "fa_fwd.hip", "fa_decode.hip", "fa_mask.hip", "fa_naive.hip", "fa_capi.hip",
+]
 
-# Packed-FP32 VALU forms are disabled for all device code.
+# Packed-FP32 VALU forms are disabled for all device code.  The atomic
+# optimizer is off: it would turn the fused kernel's single-lane ticket
+# request into a wave-wide one whose result is waited for at once, where the
+# kernel wants the request in flight during its last step.
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 
 
@@ -66,13 +78,23 @@ def ext_path() -> str:
 
 
 def build_hip_lib(verbose: bool = False) -> str:
+    """Compiles every HIP source to an object (in parallel, in a temporary
+    directory) and links the shared library."""
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     out = hip_lib_path()
     tmp = out + ".tmp"
-    cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}"]
-    cmd += [os.path.join(CSRC, s) for s in HIP_SOURCES]
-    cmd += ["-o", tmp]
-    _run(cmd, verbose)
+    objdir = tempfile.mkdtemp(prefix="fa_sm75_build_")
+    try:
+        objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in HIP_SOURCES]
+        cmds = [[hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+                 os.path.join(CSRC, s), "-o", o] for s, o in zip(HIP_SOURCES, objs)]
+        jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            for f in [pool.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+    finally:
+        shutil.rmtree(objdir, ignore_errors=True)
     os.replace(tmp, out)
     return out
 

@@ -83,7 +83,8 @@ void check_fused_shapes(const torch::Tensor& Q, const torch::Tensor& K,
 }
 
 // Runs fa_sm75_forward with a workspace from torch's caching allocator when
-// the call can use one (the split-K path).  The workspace is released when
+// the call can use one (the split-K path's partials, or the ticket counters
+// of the fused kernel's dynamic schedule).  The workspace is released when
 // this returns; the allocator only hands it out again to work ordered after
 // the launch on the same stream.
 void forward_with_workspace(fa_fwd_params& p, const torch::Tensor& Q, const char* tag) {
@@ -296,7 +297,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("abi_version", []() { return fa_sm75_abi_version(); });
   m.def("set_kernel_policy", [](int policy) {
     TORCH_CHECK(fa_sm75_set_kernel_policy(policy) == FA_OK,
-                "kernel policy must be 0 (auto), 1 (narrow) or 2 (wide), got ", policy);
+                "kernel policy must be 0 (auto), 1 (narrow), 2 (wide) or 3 (dynamic), got ",
+                policy);
   });
   m.def("get_kernel_policy", []() { return fa_sm75_get_kernel_policy(); });
 }

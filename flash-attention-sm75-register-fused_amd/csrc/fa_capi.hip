@@ -156,6 +156,8 @@ fa::FwdArgs make_args(const fa_fwd_params* p) {
   a.msb = p->mask_stride_b;
   a.msh = p->mask_stride_h;
   a.msq = p->mask_stride_q;
+  a.ctr = nullptr;
+  a.items = 0;
   return a;
 }
 
@@ -219,7 +221,12 @@ int fa_sm75_forward(const fa_fwd_params* p) {
         fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, room);
     fa::launch_decode_forward(a, plan, (int)p->head_dim, p->causal != 0, p->workspace, stream);
   } else {
-    fa::launch_fused_forward(a, (int)p->batch, (int)p->head_dim, p->causal != 0, policy,
+    fa::FwdArgs f = a;
+    // A workspace of kTicketBytes enables the dynamic (XCD-balanced) schedule;
+    // it is 8-byte aligned (16 is required of every workspace).
+    if (p->workspace != nullptr && p->workspace_bytes >= fa::kTicketBytes)
+      f.ctr = static_cast<uint64_t*>(p->workspace);
+    fa::launch_fused_forward(f, (int)p->batch, (int)p->head_dim, p->causal != 0, policy,
                              stream);
   }
   return check_launch();
@@ -231,11 +238,12 @@ int64_t fa_sm75_workspace_size(const fa_fwd_params* p) {
   std::snprintf(g_last_error, sizeof(g_last_error), "%s", saved.c_str());
   if (st != FA_OK || p->batch == 0 || p->heads_q == 0 || p->seq_len == 0) return 0;
   const fa::FwdArgs a = make_args(p);
-  if (g_kernel_policy.load(std::memory_order_relaxed) != FA_POLICY_AUTO ||
-      !fa::decode_eligible(a))
-    return 0;
-  return fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, INT64_MAX)
-      .workspace_bytes;
+  const int policy = g_kernel_policy.load(std::memory_order_relaxed);
+  if (policy == FA_POLICY_AUTO && fa::decode_eligible(a))
+    return fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, INT64_MAX)
+        .workspace_bytes;
+  // Fused kernel: the counters of the dynamic schedule (AUTO, DYNAMIC).
+  return policy == FA_POLICY_AUTO || policy == FA_POLICY_DYNAMIC ? fa::kTicketBytes : 0;
 }
 
 int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
@@ -257,7 +265,7 @@ int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t
 }
 
 int fa_sm75_set_kernel_policy(int policy) {
-  if (policy < FA_POLICY_AUTO || policy > FA_POLICY_WIDE) return FA_ERR_INVALID_ARGUMENT;
+  if (policy < FA_POLICY_AUTO || policy > FA_POLICY_DYNAMIC) return FA_ERR_INVALID_ARGUMENT;
   g_kernel_policy.store(policy, std::memory_order_relaxed);
   return FA_OK;
 }

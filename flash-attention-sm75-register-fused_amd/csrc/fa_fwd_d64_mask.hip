@@ -1,0 +1,6 @@
+// Fused forward instances: head_dim 64, 128-row workgroups (4 waves) with a boolean mask.
+#include "fa_fwd_kernel.h"
+
+namespace fa {
+template void launch_fused<64, 4, true>(const FwdArgs&, int, bool, Schedule, hipStream_t);
+}  // namespace fa

@@ -1,0 +1,649 @@
+// Fused attention forward kernel for gfx950 (MI355X / CDNA4), included by the
+// instance files fa_fwd_d*.hip (one head dimension and workgroup shape each,
+// compiled in parallel); fa_fwd.hip dispatches between them.
+//
+// O = softmax(scale * Q K^T + mask) V with fp16 inputs, fp32 accumulation and
+// an fp16 output, in one kernel (the hot path that reference
+// src/kernels/flash_attention_forward.cu:345-791 implements for SM75).
+//
+// Work decomposition
+//   A 1-D grid of batch * heads_q * ceil(N / kBlockM) workgroups, kBlockM =
+//   128 query rows each, ordered so the workgroups reading one K/V pair share
+//   an XCD (block_work in fa_kernel_common.h).
+//   One workgroup = 4 waves; wave w owns query rows [q0 + 32w, q0 + 32w + 32).
+//   Key/value rows stream through LDS in tiles of kBlockN = 64 keys.  Tiles
+//   go straight from HBM to LDS (buffer_load ... lds: lane l's 16 bytes land
+//   at M0 + 16 l), through buffer windows that end at the last key, so rows
+//   past the sequence arrive as zeros.
+//
+// MFMA formulation (v_mfma_f32_32x32x16_f16, operand layouts verified on the
+// device):
+//   A[m][k]: lane l holds m = l%32, k = 8*(l/32) + j  (8 halves)
+//   B[k][n]: lane l holds n = l%32, k = 8*(l/32) + j  (8 halves)
+//   C[m][n]: lane l holds n = l%32, m = 8*(i/4) + 4*(l/32) + i%4 (16 floats)
+//   * S^T = K Q^T: keys are the M side, queries the N side, so every lane owns
+//     a single query (l%32) and 16 of its 32 keys per 32-key sub-tile.  The
+//     row max over keys is an in-register reduction plus one lane swap
+//     between the two wave halves; the row sum stays lane-local until the end.
+//   * O^T = V^T P^T: the probabilities stay in the registers the S^T
+//     accumulator produced, reinterpreted as the B operand.  The key order
+//     inside each 16-key MFMA step is a permutation shared by P and V (the
+//     contraction is order-free).  V^T operands come straight out of a
+//     row-major LDS tile with ds_read_b64_tr_b16 (transposing LDS read).
+//   * The O^T accumulator keeps, per lane, one query and D/2 of its
+//     dimensions, so the online-softmax rescale is a per-lane scalar.
+//
+// Scheduling.  On this hardware a wave's VALU work overlaps its *own* MFMAs
+// (issued between them) but hardly overlaps MFMAs of another wave on the
+// same SIMD.  So the main loop is software pipelined and hand ordered:
+// iteration j issues the MFMAs of S_{j+1} and P_j V_j one "slot" at a time,
+// and each slot also carries the LDS reads needed a few slots later and a
+// share of the softmax of S_j (exp, fp16 pack, row sum).
+//
+// Softmax numerics follow reference src/kernels/flash_attention_forward.cu:
+// running max starts at -inf and the first rescale factor is 0 (:386,:483),
+// masked keys contribute exactly 0 (:470-479), probabilities are rounded to
+// fp16 before the PV product (:495), the final row factor is 1/l (:562).
+// exp is evaluated as 2^(x * log2 e) with the log2 e folded into the scale.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "fa_internal.h"
+
+#include "fa_kernel_common.h"
+
+namespace fa {
+namespace {
+
+// Software-pipelined main loop: step j computes S^T_{j+1} = K_{j+1} Q^T while
+// the VALU turns S^T_j into probabilities, then accumulates P_j V_j.  One
+// barrier per step.  Two shapes (WAVES):
+//   * 4 waves, 128 query rows, two workgroups per CU, K/V tiles double
+//     buffered (STAGES = 2): step j loads K_{j+2} and V_{j+1} into the
+//     buffers step j-1 freed, and they must land by the end of step j;
+//   * 8 waves, 256 query rows, one workgroup per CU, triple buffered
+//     (STAGES = 3): step j loads K_{j+3} and V_{j+2}, which have until the
+//     end of step j+1 to land; every K/V tile serves 256 query rows, and each
+//     wave issues half as many direct loads (waves 0-3 load K, 4-7 load V).
+// KV_SAME_STRIDE: K and V rows have the same stride, so the direct-load
+// offsets are shared (saves registers).  MASK: an explicit mask (one 64-bit
+// word per query row and tile, loaded a step ahead) hides keys too.
+template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, bool MASK>
+__global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
+  using L = Lds<D>;
+  constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
+  constexpr int MT = D / 32;       // 32-row output tiles of O^T
+  constexpr int NS = 2 * KK;       // S^T MFMAs per tile
+  constexpr int NPV = 4 * MT;      // P V MFMAs per tile
+  constexpr int PFK = 3;           // K operand reads run this many MFMAs ahead
+  constexpr int PFV = 2;           // V operand reads run this many MFMAs ahead
+  constexpr int BLOCK_M = 32 * WAVES;
+  constexpr int STAGES = WAVES == 8 ? 3 : 2;
+  constexpr int SEGQ = L::Segs / 4;           // segments of one tile per wave quarter
+  constexpr int LPW = 2 * L::Segs / WAVES;    // direct loads per wave per step
+  constexpr bool SPLIT_ROLES = WAVES == 8;    // a wave loads K or V, not both
+  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
+  static_assert(L::Segs % 4 == 0, "tile segments must split over 4 waves");
+
+  // STAGES K buffers and STAGES V buffers, distinct objects (not one array):
+  // the loop is unrolled by STAGES, so every access names its buffer at
+  // compile time and the compiler can see that the in-flight direct loads
+  // never alias the tiles being read (it would otherwise drain vmcnt before
+  // each LDS read).
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds0[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds1[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds2[STAGES == 3 ? L::Tile : 1];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds0[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds1[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds2[STAGES == 3 ? L::Tile : 1];
+
+  // Wave index: scalar (the direct loads' LDS destinations, M0, derive from
+  // it) and the only thread coordinate kept across work items.
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+
+  // Work items.  Static schedule (a.ctr == nullptr): workgroup wg does item
+  // wg.  Dynamic schedule (4-wave kernel, a.ctr set, grid = resident
+  // workgroups): the items form a.xcds queues, queue x holding the items the
+  // static schedule gives XCD x, in the same (largest first) order.  A
+  // workgroup takes items from the head of its own XCD's queue; once that is
+  // empty it takes from the tail (the smallest items) of the others, so XCDs
+  // running at a higher clock take over the end of slower XCDs' work
+  // without starting a long item late.  Each queue is one 64-bit counter,
+  // head count in the low word, tail count in the high word: an atomic add
+  // of 1 (head) or 2^32 (tail) claims head index h or tail index P-1-t of
+  // the counts (h, t) it returns, if h + t < P (P items per queue).  Every
+  // claim raises h + t by one, so no item is claimed twice.
+  // Thread 0 (wave 0, lane 0) claims the items (the head claim for the next
+  // item is issued at the start of the item's last step) and passes the item
+  // and the set of queues it found empty to every wave through LDS: V_1's
+  // buffer, which no direct load writes between an item's last step and the
+  // next item's step 0.
+  const bool dynamic = WAVES == 4 && a.ctr != nullptr;
+  const int nq = a.xcds;
+  const int per_queue = a.items / nq;
+  const int own_q = (int)(__builtin_amdgcn_s_getreg(kHwRegXccId) & 15u) % nq;
+  int* const ticket_slot = (int*)v_lds1;
+  auto lane_id = [] {
+    return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  };
+  auto claim = [&](int q, bool tail) -> uint64_t {
+    return __hip_atomic_fetch_add(a.ctr + q * kCtrStride, tail ? (1ull << 32) : 1ull,
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  // Item of a claim's returned counts (h, t), or -1 if the queue was empty.
+  auto claimed_item = [&](int q, bool tail, uint64_t ht) -> int {
+    const int h = (int)(uint32_t)ht, t = (int)(ht >> 32);
+    if (h + t >= per_queue) return -1;
+    return (tail ? per_queue - 1 - t : h) * nq + q;
+  };
+  // Thread 0: the next item (-1: none left), from the prefetched head claim
+  // of the own queue if there is one, else from the queues not yet empty.
+  auto take_item = [&](bool prefetched, uint64_t ht, unsigned& empty) -> int {
+    if (prefetched) {
+      const int it = claimed_item(own_q, false, ht);
+      if (it >= 0) return it;
+      empty |= 1u << own_q;
+    }
+    for (int i = 0; i < nq; ++i) {
+      const int qi = own_q + i < nq ? own_q + i : own_q + i - nq;
+      if ((empty >> qi) & 1u) continue;
+      const int it = claimed_item(qi, i != 0, claim(qi, i != 0));
+      if (it >= 0) return it;
+      empty |= 1u << qi;
+    }
+    return -1;
+  };
+  auto publish_item = [&](bool prefetched, uint64_t ht, unsigned empty) {
+    if (wave == 0 && lane_id() == 0) {
+      ticket_slot[0] = take_item(prefetched, ht, empty);
+      ticket_slot[1] = (int)empty;
+    }
+  };
+  int item = (int)blockIdx.x;
+  unsigned empty_q = 0;  // queues found exhausted (scalar, same in every wave)
+  if (dynamic) {
+    publish_item(false, 0ull, 0u);
+    __syncthreads();
+    item = __builtin_amdgcn_readfirstlane(ticket_slot[0]);
+    empty_q = (unsigned)__builtin_amdgcn_readfirstlane(ticket_slot[1]);
+  }
+  while (item >= 0) {
+    // Lane-dependent values are derived per item from an opaque lane index,
+    // so none of them is hoisted out of the item loop and kept live in VGPRs
+    // between items (the main loop needs every register).
+    int lane = lane_id();
+    asm volatile("" : "+v"(lane));
+    const int tid = wave * 64 + lane;
+    const int wq = wave & 3;    // quarter of the direct-load segments
+    const bool v_role = SPLIT_ROLES && wave >= 4;
+    const int hi = lane >> 5;   // which half of the wave
+    const int ql = lane & 31;   // query column owned by this lane
+    const int grp = lane >> 4;  // 16-lane group (transposing reads)
+    const int gi = lane & 15;
+    // Thread 0: the head claim on the own queue for the next item, issued at
+    // the start of this item's last step.
+    const bool prefetch = dynamic && !((empty_q >> own_q) & 1u);
+    uint64_t next_claim = 0ull;
+
+    const Work w = block_work(a, item, CAUSAL);
+    const int b = w.b, hq = w.hq, hkv = w.hkv, qb = w.qb;
+    const int bh = b * a.hq + hq;
+    const int q0 = qb * BLOCK_M;
+    const int qw = q0 + wave * 32;
+    const int qrow = qw + ql;
+    const int N = a.n;    // query rows
+    const int NK = a.nk;  // key rows
+
+    const _Float16* Qp = a.q + b * a.qsb + hq * a.qsh;
+    // Mask bits of this lane's query row (rows past N read row N - 1).
+    const uint64_t* mrow =
+        MASK ? a.mbits + b * a.msb + hq * a.msh + (int64_t)min(qrow, N - 1) * a.msq : nullptr;
+    const _Float16* Kp = a.k + b * a.ksb + hkv * a.ksh;
+    const _Float16* Vp = a.v + b * a.vsb + hkv * a.vsh;
+
+    // Q^T fragments (B operand of S^T = K Q^T), resident for the whole kernel.
+    half8 qf[KK];
+    if (qrow < N) {
+      const _Float16* qp = Qp + (int64_t)qrow * a.qsn + 8 * hi;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) qf[kk] = *(const half8*)(qp + 16 * kk);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) qf[kk] = (half8)(_Float16)0;
+    }
+    if (a.negate_q) {
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) qf[kk] = -qf[kk];
+    }
+
+    // Keys this block can see (none for a block entirely before the diagonal).
+    const int kv_len = CAUSAL ? max(0, min(NK, q0 + BLOCK_M + a.diag)) : NK;
+    const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
+
+    // Direct-load map: wave quarter wq fills 1 KB segments wq, wq + 4, ... of a
+    // tile; lane l of a segment covers tile bytes [1024 seg + 16 l, +16).  The
+    // global byte offset inside a tile of each segment (padding lanes: past
+    // the end).  goff_a: K (4 waves) or this wave's tile kind (8 waves);
+    // goff_b: V with its own stride (4 waves, different strides only).
+    constexpr bool OWN_B = !SPLIT_ROLES && !KV_SAME_STRIDE;
+    int goff_a[SEGQ], goff_b_own[OWN_B ? SEGQ : 1];
+    int* goff_b = OWN_B ? goff_b_own : goff_a;
+    const int64_t a_stride = v_role ? a.vsn : a.ksn;
+#pragma unroll
+    for (int s = 0; s < SEGQ; ++s) {
+      const int pos = (wq + 4 * s) * 1024 + 16 * lane;  // bytes into the tile
+      const int row = pos / (2 * L::Pitch);
+      const int within = pos - row * (2 * L::Pitch);
+      if (within < 2 * D) {
+        const int c = (within >> 4) ^ ((row >> 2) & 3);
+        goff_a[s] = (int)(row * a_stride * 2) + 16 * c;
+        if (OWN_B) goff_b[s] = (int)(row * a.vsn * 2) + 16 * c;
+      } else {
+        goff_a[s] = -16;  // 0xfffffff0: beyond any window -> writes zeros
+        if (OWN_B) goff_b[s] = -16;
+      }
+    }
+    const int k_tile_bytes = (int)(kBlockN * a.ksn * 2);
+    const int v_tile_bytes = (int)(kBlockN * a.vsn * 2);
+    const int k_all_bytes = (int)(NK * a.ksn * 2);
+    const int v_all_bytes = (int)(NK * a.vsn * 2);
+
+    // Buffer selection by compile-time stage index.
+    auto kbuf = [&](auto st) -> _Float16* {
+      constexpr int S = decltype(st)::value % STAGES;
+      if constexpr (S == 0) return k_lds0;
+      else if constexpr (S == 1) return k_lds1;
+      else return k_lds2;
+    };
+    auto vbuf = [&](auto st) -> _Float16* {
+      constexpr int S = decltype(st)::value % STAGES;
+      if constexpr (S == 0) return v_lds0;
+      else if constexpr (S == 1) return v_lds1;
+      else return v_lds2;
+    };
+    auto lds_seg = [&](_Float16* tile, int s) -> lds_void* {
+      return (lds_void*)(tile + (wq + 4 * s) * 512);
+    };
+    // Buffer windows of tile j (empty past the last tile: every lane reads 0).
+    auto k_window = [&](int j) {
+      const int bytes = k_all_bytes - j * k_tile_bytes;
+      return make_rsrc(Kp + (int64_t)j * kBlockN * a.ksn, bytes > 0 ? bytes : 0);
+    };
+    auto v_window = [&](int j) {
+      const int bytes = v_all_bytes - j * v_tile_bytes;
+      return make_rsrc(Vp + (int64_t)j * kBlockN * a.vsn, bytes > 0 ? bytes : 0);
+    };
+    // This wave's segments of K tile j (into kdst) or V tile j (into vdst).
+    auto load_tile = [&](bool is_v, int j, _Float16* dst) {
+      const __amdgpu_buffer_rsrc_t r = is_v ? v_window(j) : k_window(j);
+#pragma unroll
+      for (int s = 0; s < SEGQ; ++s)
+        direct_load16(r, lds_seg(dst, s), (is_v && OWN_B) ? goff_b[s] : goff_a[s]);
+    };
+
+    // Per-lane LDS bases of the operand reads (see Lds): K rows ql (+32t),
+    // chunk 2kk + hi; V rows 16ks + 4hi + gi/4 (+8), dims 32mt + 16(grp&1) + 4(gi&3).
+    const int sK = (ql >> 2) & 3;
+    const int k_base_even = ql * L::Pitch + 8 * (hi ^ sK);
+    const int k_base_odd = ql * L::Pitch + 8 * ((2 + hi) ^ sK);
+    const int v_row = 4 * hi + (gi >> 2);
+    const int v_c = 2 * (grp & 1) + ((gi & 3) >> 1);
+    const int v_base0 = v_row * L::Pitch + 8 * (v_c ^ hi) + 4 * (gi & 1);
+    const int v_base1 = (v_row + 8) * L::Pitch + 8 * (v_c ^ (hi + 2)) + 4 * (gi & 1);
+
+    // K operand i (sub-tile t = i / KK, step kk = i % KK) of one K buffer.
+    auto read_k = [&](const _Float16* Ks, int i) -> half8 {
+      const int t = i / KK, kk = i % KK;
+      const int off = ((kk & 1) ? k_base_odd : k_base_even) + 32 * t * L::Pitch + 32 * (kk >> 1);
+      return *(const half8*)(Ks + off);
+    };
+    // V^T operand v (16-key step ks = v / MT, output tile mt = v % MT).
+    auto read_v = [&](const _Float16* Vs, int v) -> half8 {
+      const int ks = v / MT, mt = v % MT;
+      const int imm = 16 * ks * L::Pitch + 32 * mt;
+      const half4 lo = ds_read_tr16(Vs + v_base0 + imm);
+      const half4 hi4 = ds_read_tr16(Vs + v_base1 + imm);
+      return __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+
+    float16v oacc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) oacc[mt] = (float16v)0.0f;
+    float m_run = -__builtin_inff();
+    float l_run = 0.0f;
+    const float c2 = a.c;  // |scale| * log2(e)
+    const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+
+    // S^T of two tiles in flight, ping-pong by the parity of the step's
+    // position in the unrolled loop: step u reads s_buf[u & 1] and fills the
+    // other one (with three stages, one copy per three steps restores it).
+    float16v s_buf[2][2];
+    auto row_max = [](const float16v (&s)[2]) {
+      float m0 = s[0][0], m1 = s[1][0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) {
+        m0 = fmaxf(m0, s[0][i]);
+        m1 = fmaxf(m1, s[1][i]);
+      }
+      return fmaxf(m0, m1);
+    };
+    float mc = 0.0f;  // running max of tile j's rows, times c2 (exp2 offset)
+
+    // Prepares tile j's scores for its softmax: masks them if tile j crosses
+    // the sequence end or this wave's causal diagonal, or (MASK) hides a key
+    // from some row of the wave (the unmasked row max mx is then recomputed),
+    // raises the running max when some row outgrew it by more than
+    // 2^kRescaleLog2 (rescaling O and l), and sets mc.  mw: the lane's mask
+    // word of tile j (bit k: key 64 j + k visible).
+    auto prepare = [&](int j, float16v (&s)[2], float mx, uint64_t mw) {
+      const int kstart = j * kBlockN;
+      bool need_mask =
+          (kstart + kBlockN > NK) || (CAUSAL && kstart + kBlockN - 1 > qw + a.diag);
+      if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
+      if (need_mask) {
+        const uint64_t mws = mw >> (4 * hi);  // bit 32 t + 8 (i / 4) + i % 4: element (t, i)
+        // static_for: a loop the unroller leaves rolled would index s at run
+        // time and move the score registers to scratch memory.
+        static_for<32>([&](auto e_c) {
+          constexpr int e = decltype(e_c)::value;
+          constexpr int t = e >> 4, i = e & 15;
+          const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
+          bool masked = (key >= NK) || (CAUSAL && key > qrow + a.diag);
+          if (MASK) masked = masked || ((mws >> (32 * t + 8 * (i >> 2) + (i & 3))) & 1) == 0;
+          if (masked) s[t][i] = -__builtin_inff();
+        });
+        mx = halves_max(row_max(s));
+      }
+      const bool grow = (mx - m_run) * c2 > kRescaleLog2;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
+        const float alpha =
+            (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * c2);
+        l_run *= alpha;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) oacc[mt] *= alpha;
+        m_run = m_new;
+      }
+      mc = ((m_run == -__builtin_inff()) ? 0.0f : m_run) * c2;
+    };
+
+    // One pipeline step for tile j, at position U of the unrolled loop (its
+    // V tile is in buffer U % STAGES), whose scores are prepared.  HAS_NEXT:
+    // tile j+1 exists, so S_{j+1} is computed (and prepared) here and the
+    // loads of K_{j+STAGES} and V_{j+STAGES-1} are issued.
+    auto step = [&](int j, auto has_next_t, auto u_t) {
+      constexpr bool HAS_NEXT = decltype(has_next_t)::value;
+      constexpr int U = decltype(u_t)::value;
+      if constexpr (!HAS_NEXT) {
+        if (prefetch && tid == 0) next_claim = claim(own_q, false);
+      }
+      constexpr int PAR = U & 1;
+      constexpr int ns = HAS_NEXT ? NS : 0;     // S MFMAs this step
+      const _Float16* Kn = kbuf(std::integral_constant<int, U + 1>{});
+      const _Float16* Vc = vbuf(std::integral_constant<int, U>{});
+      float16v (&s_cur)[2] = s_buf[PAR];
+      float16v (&s_nxt)[2] = s_buf[1 - PAR];
+
+      // Direct loads of K_{j+STAGES} (into the buffer K_j used) and
+      // V_{j+STAGES-1} (into the buffer V_{j-1} used), one 1 KB segment after
+      // each of the first MFMAs, so the address unit's queueing overlaps MFMA
+      // execution.  Past the last tile the windows are empty.
+      __amdgpu_buffer_rsrc_t rk_next, rv_next;
+      uint64_t mw_next = ~0ull;
+      if (HAS_NEXT) {
+        rk_next = k_window(j + STAGES);
+        rv_next = v_window(j + STAGES - 1);
+        if (MASK) mw_next = mrow[j + 1];  // consumed by prepare(j + 1) at the end
+      }
+      _Float16* k_dst = kbuf(std::integral_constant<int, U>{});
+      _Float16* v_dst = vbuf(std::integral_constant<int, U + STAGES - 1>{});
+      auto issue_load = [&](int q) {
+        if constexpr (SPLIT_ROLES) {  // q < SEGQ: segment q of this wave's tile kind
+          direct_load16(v_role ? rv_next : rk_next, lds_seg(v_role ? v_dst : k_dst, q), goff_a[q]);
+        } else {  // q < SEGQ: K segment q, else V segment q - SEGQ
+          if (q < SEGQ)
+            direct_load16(rk_next, lds_seg(k_dst, q), goff_a[q]);
+          else
+            direct_load16(rv_next, lds_seg(v_dst, q - SEGQ), goff_b[q - SEGQ]);
+        }
+      };
+
+      // ---- slots: S_{j+1} MFMAs, then P_j V_j --------------------------------
+      // The softmax of S_j (16 pairs of scores) is spread over the slots.
+      // Within a slot the MFMA is issued first, so the pairs of 16-key step ks
+      // must sit in a slot before the first P V MFMA of step ks; pairs that
+      // cannot (the last tile has no S MFMAs to hide them behind) go first.
+      constexpr int NB = ns + NPV;                    // MFMA slots
+      constexpr int PV_FIRST = ns;                    // slot of the first P V MFMA
+      constexpr int PAIR_SLOTS = NB - MT;             // slots available to pairs
+      half8 kf[NS];
+      half8 pf[4];
+      half8 vf[NPV];
+      constexpr auto pair_slot = [](int p) constexpr {
+        const int spread = (p * PAIR_SLOTS) / 16;
+        const int last_ok = PV_FIRST + (p / 4) * MT - 1;
+        return spread < last_ok ? spread : last_ok;
+      };
+      // Row max of S_{j+1}: element e (sub-tile t = e / 16) is folded in at
+      // max_slot(e), a few slots after the last MFMA into sub-tile t; the lane
+      // swap of the two wave halves sits in the last slot.
+      constexpr auto max_slot = [](int e) constexpr {
+        const int t = e >> 4, i = e & 15;
+        const int first = (t + 1) * KK + 2;
+        const int span = (t == 0 ? KK : NB - 1 - first);
+        const int s = first + (i * span) / 16;
+        return s < NB - 1 ? s : NB - 1;
+      };
+      auto softmax_pair = [&](auto p_c) {
+        constexpr int p = decltype(p_c)::value;
+        constexpr int e = 2 * p;
+        constexpr int t = e >> 4, i = e & 15;
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i], c2, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i + 1], c2, -mc));
+        const half2v pr = {(_Float16)p0, (_Float16)p1};
+        pf[2 * t + (i >> 3)][i & 7] = pr[0];
+        pf[2 * t + (i >> 3)][(i & 7) + 1] = pr[1];
+        l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
+      };
+      static_for<16>([&](auto p_c) {
+        if constexpr (pair_slot(decltype(p_c)::value) < 0) softmax_pair(p_c);
+      });
+      static_for<(PFK < ns ? PFK : ns)>([&](auto i_c) {
+        kf[decltype(i_c)::value] = read_k(Kn, decltype(i_c)::value);
+      });
+      float mx_next = -__builtin_inff();
+      static_for<NB>([&](auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value;
+        // V operand reads, PFV MFMAs ahead of their use
+        if constexpr (slot == (PV_FIRST >= PFV ? PV_FIRST - PFV : 0)) {
+          static_for<PFV>([&](auto v_c) {
+            vf[decltype(v_c)::value] = read_v(Vc, decltype(v_c)::value);
+          });
+        }
+        if constexpr (slot >= PV_FIRST && slot - PV_FIRST + PFV < NPV) {
+          vf[slot - PV_FIRST + PFV] = read_v(Vc, slot - PV_FIRST + PFV);
+        }
+        // the MFMA of this slot
+        if constexpr (slot < PV_FIRST) {
+          constexpr int i = slot;
+          if constexpr (i + PFK < ns) kf[i + PFK] = read_k(Kn, i + PFK);
+          constexpr int t = i / KK, kk = i % KK;
+          s_nxt[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              kf[i], qf[kk], kk == 0 ? (float16v)0.0f : s_nxt[t], 0, 0, 0);
+        } else {
+          constexpr int v = slot - PV_FIRST;
+          constexpr int ks = v / MT, mt = v % MT;
+          oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[v], pf[ks], oacc[mt], 0, 0, 0);
+        }
+        if constexpr (HAS_NEXT) {
+          static_for<LPW>([&](auto q_c) {
+            constexpr int q = decltype(q_c)::value;
+            if constexpr ((q * (NB / 2)) / LPW == slot) issue_load(q);
+          });
+          static_for<32>([&](auto e_c) {
+            constexpr int e = decltype(e_c)::value;
+            if constexpr (max_slot(e) == slot) mx_next = fmaxf(mx_next, s_nxt[e >> 4][e & 15]);
+          });
+          if constexpr (slot == NB - 1) mx_next = halves_max(mx_next);
+        }
+        static_for<16>([&](auto p_c) {
+          if constexpr (pair_slot(decltype(p_c)::value) == slot) softmax_pair(p_c);
+        });
+        fence_schedule();
+      });
+
+      if (HAS_NEXT) {
+        prepare(j + 1, s_nxt, mx_next, mw_next);
+        // The loads of the previous step have landed (those of this step may
+        // still be in flight with three stages), and every wave is done with
+        // the buffers the next step's loads overwrite.
+        barrier_after_loads<STAGES == 3 ? LPW : 0>();
+      }
+    };
+
+    // ---- prologue: K_0..K_{STAGES-1} and V_0..V_{STAGES-2} into LDS; S_0 -----
+    if (ntiles > 0) {
+      static_for<STAGES>([&](auto t_c) {
+        if (!v_role) load_tile(false, decltype(t_c)::value, kbuf(t_c));
+      });
+      static_for<STAGES - 1>([&](auto t_c) {
+        if (!SPLIT_ROLES || v_role) load_tile(true, decltype(t_c)::value, vbuf(t_c));
+      });
+    }
+    barrier_after_loads<0>();
+    if (ntiles > 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        s_buf[0][t] = (float16v)0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          s_buf[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(k_lds0, t * KK + kk), qf[kk],
+                                                               s_buf[0][t], 0, 0, 0);
+      }
+      prepare(0, s_buf[0], halves_max(row_max(s_buf[0])), MASK ? mrow[0] : ~0ull);
+      // Step 0 loads K_STAGES into K_0's buffer: every wave must be done
+      // reading it for S_0 first.
+      __syncthreads();
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      int j = 0;
+      for (; j + STAGES < ntiles; j += STAGES) {  // every step has a next tile
+        step(j, Flag<true>{}, I0{});
+        step(j + 1, Flag<true>{}, I1{});
+        if constexpr (STAGES == 3) {
+          step(j + 2, Flag<true>{}, I2{});
+          s_buf[0][0] = s_buf[1][0];
+          s_buf[0][1] = s_buf[1][1];
+        }
+      }
+      const int rest = ntiles - j;  // 1 .. STAGES steps left, the last one without a next tile
+      if (rest == 1) {
+        step(j, Flag<false>{}, I0{});
+      } else if (STAGES == 2 || rest == 2) {
+        step(j, Flag<true>{}, I0{});
+        step(j + 1, Flag<false>{}, I1{});
+      } else if constexpr (STAGES == 3) {
+        step(j, Flag<true>{}, I0{});
+        step(j + 1, Flag<true>{}, I1{});
+        step(j + 2, Flag<false>{}, I2{});
+      }
+    }
+    // No direct load may land in LDS after the workgroup ends.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+
+    // ---- epilogue: combine the two half-wave partial sums, normalise, store ---
+    const float l_tot = halves_sum(l_run);
+    const float inv = (l_tot > 0.0f) ? (1.0f / l_tot) : 0.0f;
+    if (qrow < N) {
+      _Float16* op = a.o + b * a.osb + hq * a.osh + (int64_t)qrow * a.osn;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          half4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (_Float16)(oacc[mt][4 * g + e] * inv);
+          *(half4*)(op + 32 * mt + 8 * g + 4 * hi) = v;
+        }
+      }
+      if (a.lse != nullptr && hi == 0) {
+        const float m_use = (m_run == -__builtin_inff()) ? 0.0f : m_run;
+        const float lse2 = m_use * c2 + __builtin_log2f(l_tot);
+        a.lse[(int64_t)bh * N + qrow] = lse2 * 0.69314718055994530942f;
+      }
+    }
+    if (!dynamic) break;
+    // Next item: every wave is past its last LDS read of this item's tiles.
+    __syncthreads();
+    publish_item(prefetch && ntiles > 0, next_claim, empty_q);
+    __syncthreads();
+    item = __builtin_amdgcn_readfirstlane(ticket_slot[0]);
+    empty_q = (unsigned)__builtin_amdgcn_readfirstlane(ticket_slot[1]);
+  }
+}
+
+}  // namespace
+
+// Launches fa_fwd_kernel<D, ...> for one workgroup shape and mask mode; the
+// causal flag and K/V stride equality pick the instance.
+// Key tiles all query blocks of one (batch, head) step through.
+inline int64_t tile_steps_per_head(const FwdArgs& a, bool causal, int block_m) {
+  const int64_t full = ((int64_t)a.nk + kBlockN - 1) / kBlockN;
+  if (!causal) return full * a.num_qblocks;
+  int64_t steps = 0;
+  for (int qb = 0; qb < a.num_qblocks; ++qb) {
+    const int64_t kv = std::min<int64_t>(a.nk, std::max<int64_t>(0, (int64_t)qb * block_m +
+                                                                        block_m + a.diag));
+    steps += (kv + kBlockN - 1) / kBlockN;
+  }
+  return steps;
+}
+
+// Ticket counters (a.ctr) enable the dynamic schedule of the 4-wave kernel
+// for long launches: at least kDynamicMinSteps tile steps per resident
+// workgroup (about 2 ms at C5 scale).  It evens out XCDs that run at
+// different clocks, which only pays off once their drift over the launch
+// exceeds the per-item cost of claiming work (measured on MI355X: +2.5-4.6%
+// for B=2 Hq=64 N=16384 d=128 causal, neutral for N=8192, 2-5% slower for
+// launches of short items).  The counters are cleared, and the grid is one
+// workgroup per resident slot.
+constexpr int64_t kDynamicMinSteps = 1024;
+
+template <int D, int WAVES, bool MASK>
+void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
+                  hipStream_t stream) {
+  const bool same = a.ksn == a.vsn;
+  FwdArgs args = a;
+  int64_t wgs = plan_grid(args, batch, 32 * WAVES);
+  const int64_t slots = resident_fused_workgroups();
+  const bool dynamic =
+      WAVES == 4 && args.ctr != nullptr &&
+      (schedule == Schedule::kDynamic ||
+       (schedule == Schedule::kAuto && wgs > slots &&
+        (int64_t)batch * args.hq * tile_steps_per_head(args, causal, 32 * WAVES) >=
+            kDynamicMinSteps * slots));
+  if (dynamic) {
+    launch_clear_tickets(args.ctr, stream);
+    wgs = std::min(wgs, slots);
+  } else {
+    args.ctr = nullptr;
+  }
+  const dim3 grid((unsigned)wgs);
+  const dim3 block(64 * WAVES);
+#define FA_LAUNCH(C, S) \
+  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK>), grid, block, 0, stream, args)
+  if (causal) {
+    if (same) FA_LAUNCH(true, true); else FA_LAUNCH(true, false);
+  } else {
+    if (same) FA_LAUNCH(false, true); else FA_LAUNCH(false, false);
+  }
+#undef FA_LAUNCH
+}
+
+}  // namespace fa

@@ -33,13 +33,35 @@ struct FwdArgs {
   int negate_q;     // scale < 0: Q fragments are negated (exact in fp16)
   const uint64_t* mbits;   // explicit mask bits or nullptr (see fa_fwd_params)
   int64_t msb, msh, msq;   // its strides in 64-bit words
+  uint64_t* ctr;    // queue counters of the dynamic schedule, or nullptr (static)
+  int items;        // work items (query blocks): filled by the launcher
 };
 
+// Dynamic schedule of the fused kernel: one 64-bit (head, tail) counter per
+// XCD queue, kCtrStride counters (256 bytes) apart, in a caller workspace of
+// kTicketBytes.
+constexpr int kCtrStride = 32;
+constexpr int64_t kTicketBytes = (int64_t)kNumXcds * kCtrStride * 8;
+// Workgroups of the 4-wave fused kernel resident on the current device at once
+// (two per CU); the dynamic schedule launches this many.
+int resident_fused_workgroups();
+// Zeroes the ticket counters (a small kernel, so the call stays capturable).
+void launch_clear_tickets(uint64_t* ctr, hipStream_t stream);
+
 // Launches the fused MFMA kernel; all arguments already validated.
-// policy: 0 = automatic and 1 = 128-row workgroups of 4 waves (two per CU),
-// 2 = 256-row workgroups of 8 waves (one per CU, K/V triple-buffered).
+// policy (fa_kernel_policy): 0 = automatic, 1 = 128-row workgroups of 4
+// waves (two per CU) on the static schedule, 2 = 256-row workgroups of 8
+// waves (one per CU, K/V triple-buffered), 3 = 128-row workgroups on the
+// dynamic schedule (when a.ctr is set).
 int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
                          int policy, hipStream_t stream);
+// Schedules of the 4-wave kernel: the long-launch rule, or forced.
+enum class Schedule { kAuto, kStatic, kDynamic };
+// One instance family of the fused kernel (fa_fwd_kernel.h), explicitly
+// instantiated in fa_fwd_d{64,128}{,_w8,_mask}.hip.
+template <int D, int WAVES, bool MASK>
+void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
+                  hipStream_t stream);
 int fused_block_m();  // rows of the smallest workgroup (grid-size checks)
 
 // Split-K path for few query rows per K/V head (fa_decode.hip): taken when

@@ -80,11 +80,15 @@ typedef struct fa_fwd_params {
   int causal;        /* an fa_causal value */
   void* stream;      /* hipStream_t; NULL selects the default stream */
   int64_t seq_len_kv; /* key/value rows Nk; 0 means Nk = seq_len */
-  void* workspace;    /* optional device scratch for the split-K path (few query
-                         rows per K/V head, e.g. KV-cache decode), or NULL */
+  void* workspace;    /* optional device scratch, or NULL: the split-K path's
+                         partials (few query rows per K/V head, e.g. KV-cache
+                         decode), or the fused kernel's ticket counters (its
+                         dynamic, XCD-balanced schedule).  Contents on entry
+                         do not matter; calls that share one race */
   int64_t workspace_bytes; /* its size; fa_sm75_workspace_size() gives the
                          amount for full parallelism.  With less, the call
-                         still runs, on fewer workgroups, and allocates nothing */
+                         still runs (fewer workgroups, or the static schedule)
+                         and allocates nothing */
   /* Optional explicit mask (torch SDPA's boolean attn_mask), or NULL: bit k
    * of word w of row (b, h, i) set <=> key 64w + k is visible to query i of
    * query head h in batch b; fa_sm75_pack_mask builds it.  Strides are in
@@ -138,11 +142,20 @@ int fa_sm75_abi_version(void);
 
 /* Fused-kernel selection, process-wide (no reference counterpart: a tuning
  * and testing control).  AUTO picks by problem size (the split-K path for
- * few query rows per K/V head, else 128-row workgroups); NARROW forces
- * 128-row workgroups of 4 waves (two workgroups per CU); WIDE forces 256-row
- * workgroups of 8 waves (one per CU, K/V tiles triple-buffered).  All
- * kernels compute the same function. */
-enum fa_kernel_policy { FA_POLICY_AUTO = 0, FA_POLICY_NARROW = 1, FA_POLICY_WIDE = 2 };
+ * few query rows per K/V head, else 128-row workgroups, with the dynamic
+ * XCD-balanced schedule for long launches when p->workspace holds its
+ * counters); NARROW forces 128-row workgroups of 4 waves (two workgroups per
+ * CU) on the static schedule (one workgroup per query block); WIDE forces
+ * 256-row workgroups of 8 waves (one per CU, K/V tiles triple-buffered);
+ * DYNAMIC forces 128-row workgroups on the dynamic schedule whenever the
+ * workspace holds its counters.  All compute the same function (the
+ * schedules bitwise so). */
+enum fa_kernel_policy {
+  FA_POLICY_AUTO = 0,
+  FA_POLICY_NARROW = 1,
+  FA_POLICY_WIDE = 2,
+  FA_POLICY_DYNAMIC = 3
+};
 int fa_sm75_set_kernel_policy(int policy); /* FA_OK or FA_ERR_INVALID_ARGUMENT */
 int fa_sm75_get_kernel_policy(void);
 #define FA_SM75_ABI_VERSION 2

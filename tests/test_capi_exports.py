@@ -134,9 +134,18 @@ def test_naive_validation(lib):
 def test_workspace_size(lib):
     lib.fa_sm75_workspace_size.argtypes = [ctypes.POINTER(Params)]
     lib.fa_sm75_workspace_size.restype = ctypes.c_int64
-    # prefill-sized call: the 128-row kernel needs no workspace
+    # prefill-sized call: 8 queue counters, 256 bytes apart, for the dynamic
+    # schedule of the 128-row kernel (AUTO and DYNAMIC); none for the static
+    # schedules (NARROW, WIDE)
     p = make(lib)
-    assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == 0
+    assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == 8 * 256
+    lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
+    try:
+        for policy, want in ((1, 0), (2, 0), (3, 8 * 256)):
+            lib.fa_sm75_set_kernel_policy(policy)
+            assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == want, policy
+    finally:
+        lib.fa_sm75_set_kernel_policy(0)
     # decode: 4 query heads over 2 KV heads, one query row, 8192 keys
     p = make(lib, seq_len=1, seq_len_kv=8192)
     lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
@@ -149,10 +158,11 @@ def test_workspace_size(lib):
     assert lib.fa_sm75_workspace_size(ctypes.byref(make(lib, head_dim=48, seq_len=1))) == 0
     assert lib.fa_sm75_last_error() == msg
     # a forced kernel policy never takes the split-K path
-    lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
     try:
         lib.fa_sm75_set_kernel_policy(1)
         assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == 0
+        lib.fa_sm75_set_kernel_policy(3)
+        assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == 8 * 256
     finally:
         lib.fa_sm75_set_kernel_policy(0)
 
@@ -191,10 +201,10 @@ def test_abi_version(lib):
 def test_kernel_policy_switch(lib):
     lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
     assert lib.fa_sm75_get_kernel_policy() == 0
-    assert lib.fa_sm75_set_kernel_policy(3) == 1
+    assert lib.fa_sm75_set_kernel_policy(4) == 1
     assert lib.fa_sm75_set_kernel_policy(-1) == 1
     try:
-        for p in (1, 2, 0):
+        for p in (1, 2, 3, 0):
             assert lib.fa_sm75_set_kernel_policy(p) == 0
             assert lib.fa_sm75_get_kernel_policy() == p
     finally:
