@@ -242,8 +242,8 @@ int64_t fa_sm75_workspace_size(const fa_fwd_params* p) {
   if (policy == FA_POLICY_AUTO && fa::decode_eligible(a))
     return fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, INT64_MAX)
         .workspace_bytes;
-  // Fused kernel: the counters of the dynamic schedule (AUTO, DYNAMIC).
-  return policy == FA_POLICY_AUTO || policy == FA_POLICY_DYNAMIC ? fa::kTicketBytes : 0;
+  // Fused kernel: the counters of the dynamic schedule, when it would run.
+  return fa::fused_workspace_bytes(a, (int)p->batch, p->causal != 0, policy);
 }
 
 int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,

@@ -5,6 +5,7 @@
 // parallel; this file picks the instance for a call.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include "fa_internal.h"
@@ -35,8 +36,7 @@ void launch_waves(const FwdArgs& a, int batch, int head_dim, bool causal, Schedu
 // Masked calls always take the 4-wave kernel.
 int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
                          int policy, hipStream_t stream) {
-  const Schedule schedule =
-      policy == 3 ? Schedule::kDynamic : policy == 0 ? Schedule::kAuto : Schedule::kStatic;
+  const Schedule schedule = schedule_of_policy(policy);
   if (a.mbits != nullptr)
     launch_waves<4, true>(a, batch, head_dim, causal, schedule, stream);
   else if (policy == 2)
@@ -62,6 +62,48 @@ int resident_fused_workgroups() {
     cached[dev].store(n, std::memory_order_relaxed);
   }
   return n;
+}
+
+namespace {
+
+// Key tiles all query blocks of one (batch, head) step through (64-key
+// tiles, 128-row blocks).
+int64_t tile_steps_per_head(const FwdArgs& a, bool causal) {
+  const int64_t full = ((int64_t)a.nk + 63) / 64;
+  if (!causal) return full * a.num_qblocks;
+  int64_t steps = 0;
+  for (int qb = 0; qb < a.num_qblocks; ++qb) {
+    const int64_t kv = std::min<int64_t>(a.nk, std::max<int64_t>(0, (int64_t)qb * 128 + 128 +
+                                                                        a.diag));
+    steps += (kv + 63) / 64;
+  }
+  return steps;
+}
+
+// AUTO runs the dynamic schedule for long launches only: at least
+// kDynamicMinSteps tile steps per resident workgroup (about 2 ms at C5
+// scale).  It evens out XCDs that run at different clocks, which pays off
+// once their drift over the launch exceeds the per-item cost of claiming
+// work (measured on MI355X: +2.5-4.6% for B=2 Hq=64 N=16384 d=128 causal,
+// neutral at N=8192, 2-5% slower for launches of short items).
+constexpr int64_t kDynamicMinSteps = 1024;
+
+}  // namespace
+
+bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedule schedule) {
+  if (schedule == Schedule::kDynamic) return true;
+  if (schedule != Schedule::kAuto) return false;
+  const int64_t slots = resident_fused_workgroups();
+  return planned.items > slots &&
+         (int64_t)batch * planned.hq * tile_steps_per_head(planned, causal) >=
+             kDynamicMinSteps * slots;
+}
+
+int64_t fused_workspace_bytes(const FwdArgs& a, int batch, bool causal, int policy) {
+  FwdArgs planned = a;
+  plan_grid(planned, batch, 128);
+  return use_dynamic_schedule(planned, batch, causal, schedule_of_policy(policy)) ? kTicketBytes
+                                                                                 : 0;
 }
 
 void launch_clear_tickets(uint64_t* ctr, hipStream_t stream) {

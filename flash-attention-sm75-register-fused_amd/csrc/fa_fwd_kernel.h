@@ -592,45 +592,18 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
 
 // Launches fa_fwd_kernel<D, ...> for one workgroup shape and mask mode; the
 // causal flag and K/V stride equality pick the instance.
-// Key tiles all query blocks of one (batch, head) step through.
-inline int64_t tile_steps_per_head(const FwdArgs& a, bool causal, int block_m) {
-  const int64_t full = ((int64_t)a.nk + kBlockN - 1) / kBlockN;
-  if (!causal) return full * a.num_qblocks;
-  int64_t steps = 0;
-  for (int qb = 0; qb < a.num_qblocks; ++qb) {
-    const int64_t kv = std::min<int64_t>(a.nk, std::max<int64_t>(0, (int64_t)qb * block_m +
-                                                                        block_m + a.diag));
-    steps += (kv + kBlockN - 1) / kBlockN;
-  }
-  return steps;
-}
-
-// Ticket counters (a.ctr) enable the dynamic schedule of the 4-wave kernel
-// for long launches: at least kDynamicMinSteps tile steps per resident
-// workgroup (about 2 ms at C5 scale).  It evens out XCDs that run at
-// different clocks, which only pays off once their drift over the launch
-// exceeds the per-item cost of claiming work (measured on MI355X: +2.5-4.6%
-// for B=2 Hq=64 N=16384 d=128 causal, neutral for N=8192, 2-5% slower for
-// launches of short items).  The counters are cleared, and the grid is one
-// workgroup per resident slot.
-constexpr int64_t kDynamicMinSteps = 1024;
-
+// The dynamic schedule (use_dynamic_schedule) needs ticket counters in
+// a.ctr; they are cleared first, and the grid is one workgroup per resident
+// slot.
 template <int D, int WAVES, bool MASK>
 void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream) {
   const bool same = a.ksn == a.vsn;
   FwdArgs args = a;
   int64_t wgs = plan_grid(args, batch, 32 * WAVES);
-  const int64_t slots = resident_fused_workgroups();
-  const bool dynamic =
-      WAVES == 4 && args.ctr != nullptr &&
-      (schedule == Schedule::kDynamic ||
-       (schedule == Schedule::kAuto && wgs > slots &&
-        (int64_t)batch * args.hq * tile_steps_per_head(args, causal, 32 * WAVES) >=
-            kDynamicMinSteps * slots));
-  if (dynamic) {
+  if (WAVES == 4 && args.ctr != nullptr && use_dynamic_schedule(args, batch, causal, schedule)) {
     launch_clear_tickets(args.ctr, stream);
-    wgs = std::min(wgs, slots);
+    wgs = std::min<int64_t>(wgs, resident_fused_workgroups());
   } else {
     args.ctr = nullptr;
   }

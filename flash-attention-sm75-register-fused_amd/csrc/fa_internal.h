@@ -57,6 +57,26 @@ int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
                          int policy, hipStream_t stream);
 // Schedules of the 4-wave kernel: the long-launch rule, or forced.
 enum class Schedule { kAuto, kStatic, kDynamic };
+inline Schedule schedule_of_policy(int policy) {
+  return policy == 3 ? Schedule::kDynamic : policy == 0 ? Schedule::kAuto : Schedule::kStatic;
+}
+
+// Fills num_qblocks, units, xcds and items of the fused kernel's work plan
+// for query blocks of block_m rows; returns the number of work items (the
+// grid size of the static schedule).
+inline int64_t plan_grid(FwdArgs& a, int batch, int block_m) {
+  a.num_qblocks = (int)(((int64_t)a.n + block_m - 1) / block_m);
+  a.units = batch * (a.hq / a.group);
+  a.xcds = a.units % kNumXcds == 0 ? kNumXcds : 1;
+  a.items = batch * a.hq * a.num_qblocks;
+  return a.items;
+}
+// Whether the 4-wave kernel runs the dynamic schedule for a planned call
+// (plan_grid done, 128-row blocks), given counters to run it with.
+bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedule schedule);
+// Workspace bytes the fused path uses for a call (the dynamic schedule's
+// counters, or 0), under a kernel policy.
+int64_t fused_workspace_bytes(const FwdArgs& a, int batch, bool causal, int policy);
 // One instance family of the fused kernel (fa_fwd_kernel.h), explicitly
 // instantiated in fa_fwd_d{64,128}{,_w8,_mask}.hip.
 template <int D, int WAVES, bool MASK>

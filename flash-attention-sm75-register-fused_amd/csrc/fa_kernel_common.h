@@ -145,16 +145,6 @@ __device__ __forceinline__ Work block_work(const FwdArgs& a, int wg, bool causal
   return w;
 }
 
-// Host side: fills num_qblocks, units, xcds and items, returns the number of
-// work items (the grid size of the static schedule).
-inline int64_t plan_grid(FwdArgs& a, int batch, int block_m) {
-  a.num_qblocks = (int)(((int64_t)a.n + block_m - 1) / block_m);
-  a.units = batch * (a.hq / a.group);
-  a.xcds = a.units % kNumXcds == 0 ? kNumXcds : 1;
-  a.items = batch * a.hq * a.num_qblocks;
-  return a.items;
-}
-
 // s_getreg operand for the XCC_ID hardware register (id 20, bits [31:0]):
 // its low bits name the XCD the wave runs on.
 constexpr int kHwRegXccId = 20 | (31 << 11);

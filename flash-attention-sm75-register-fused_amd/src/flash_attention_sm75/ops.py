@@ -41,16 +41,20 @@ def _check_gqa_heads(Q: torch.Tensor, K: torch.Tensor) -> None:
         )
 
 
+def _fused_forward(Q, K, V, causal, scale):
+    _check_gqa_heads(Q, K)
+    Q = Q.contiguous()
+    K = K.contiguous()
+    V = V.contiguous()
+    return Q, K, V, _C.flash_attention_forward(Q, K, V, bool(causal), float(scale))
+
+
 class FlashAttentionSM75Function(torch.autograd.Function):
     """Forward-only autograd function (reference ops.py:30-52)."""
 
     @staticmethod
     def forward(ctx, Q, K, V, causal, scale):
-        _check_gqa_heads(Q, K)
-        Q = Q.contiguous()
-        K = K.contiguous()
-        V = V.contiguous()
-        out = _C.flash_attention_forward(Q, K, V, bool(causal), float(scale))
+        Q, K, V, out = _fused_forward(Q, K, V, causal, scale)
         ctx.save_for_backward(Q, K, V, out)
         return out
 
@@ -89,7 +93,11 @@ def flash_attention_forward(Q, K, V, causal=False, scale=None):
     head_dim = _check_inputs(Q)
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
-    return FlashAttentionSM75Function.apply(Q, K, V, causal, scale)
+    if torch.is_grad_enabled() and (Q.requires_grad or K.requires_grad or V.requires_grad):
+        return FlashAttentionSM75Function.apply(Q, K, V, causal, scale)
+    # No graph is recorded for these inputs: the same forward without the
+    # autograd Function's per-call cost (inference, e.g. under no_grad).
+    return _fused_forward(Q, K, V, causal, scale)[3]
 
 
 def flash_attention_forward_lse(Q, K, V, causal=False, scale=None):

@@ -134,16 +134,24 @@ def test_naive_validation(lib):
 def test_workspace_size(lib):
     lib.fa_sm75_workspace_size.argtypes = [ctypes.POINTER(Params)]
     lib.fa_sm75_workspace_size.restype = ctypes.c_int64
-    # prefill-sized call: 8 queue counters, 256 bytes apart, for the dynamic
-    # schedule of the 128-row kernel (AUTO and DYNAMIC); none for the static
-    # schedules (NARROW, WIDE)
+    # prefill: 8 queue counters, 256 bytes apart, when the 128-row kernel's
+    # dynamic schedule runs -- under AUTO for long launches only (at least
+    # 1024 key-tile steps per resident workgroup; 512 workgroups without a
+    # device), always under DYNAMIC, never under NARROW or WIDE
     p = make(lib)
-    assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == 8 * 256
+    assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == 0
+    long_call = make(lib, batch=2, heads_q=64, heads_kv=8, seq_len=16384, causal=1)
+    lib.fa_sm75_set_contiguous_strides(ctypes.byref(long_call))
+    assert lib.fa_sm75_workspace_size(ctypes.byref(long_call)) == 8 * 256
+    short_call = make(lib, batch=1, heads_q=32, heads_kv=8, seq_len=8192, causal=1)
+    lib.fa_sm75_set_contiguous_strides(ctypes.byref(short_call))
+    assert lib.fa_sm75_workspace_size(ctypes.byref(short_call)) == 0
     lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
     try:
         for policy, want in ((1, 0), (2, 0), (3, 8 * 256)):
             lib.fa_sm75_set_kernel_policy(policy)
             assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == want, policy
+            assert lib.fa_sm75_workspace_size(ctypes.byref(long_call)) == want, policy
     finally:
         lib.fa_sm75_set_kernel_policy(0)
     # decode: 4 query heads over 2 KV heads, one query row, 8192 keys
