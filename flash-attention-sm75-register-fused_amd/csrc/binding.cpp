@@ -297,7 +297,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("abi_version", []() { return fa_sm75_abi_version(); });
   m.def("set_kernel_policy", [](int policy) {
     TORCH_CHECK(fa_sm75_set_kernel_policy(policy) == FA_OK,
-                "kernel policy must be 0 (auto), 1 (narrow), 2 (wide) or 3 (dynamic), got ",
+                "kernel policy must be 0 (auto), 1 (narrow), 2 (wide), 3 (dynamic) or 4 (split), got ",
                 policy);
   });
   m.def("get_kernel_policy", []() { return fa_sm75_get_kernel_policy(); });

@@ -243,7 +243,7 @@ int64_t fa_sm75_workspace_size(const fa_fwd_params* p) {
     return fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, INT64_MAX)
         .workspace_bytes;
   // Fused kernel: the counters of the dynamic schedule, when it would run.
-  return fa::fused_workspace_bytes(a, (int)p->batch, p->causal != 0, policy);
+  return fa::fused_workspace_bytes(a, (int)p->batch, (int)p->head_dim, p->causal != 0, policy);
 }
 
 int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
@@ -265,7 +265,7 @@ int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t
 }
 
 int fa_sm75_set_kernel_policy(int policy) {
-  if (policy < FA_POLICY_AUTO || policy > FA_POLICY_DYNAMIC) return FA_ERR_INVALID_ARGUMENT;
+  if (policy < FA_POLICY_AUTO || policy > FA_POLICY_SPLIT) return FA_ERR_INVALID_ARGUMENT;
   g_kernel_policy.store(policy, std::memory_order_relaxed);
   return FA_OK;
 }

@@ -1,7 +1,7 @@
 // Fused attention forward for gfx950 (MI355X / CDNA4): kernel selection.
 //
 // The kernel itself (fa_fwd_kernel.h) is instantiated per head dimension and
-// workgroup shape in fa_fwd_d{64,128}{,_w8,_mask}.hip, which compile in
+// workgroup shape in fa_fwd_d*.hip, which compile in
 // parallel; this file picks the instance for a call.
 #include <hip/hip_runtime.h>
 
@@ -22,9 +22,9 @@ template <int WAVES, bool MASK>
 void launch_waves(const FwdArgs& a, int batch, int head_dim, bool causal, Schedule schedule,
                   hipStream_t stream) {
   if (head_dim == 128)
-    launch_fused<128, WAVES, MASK>(a, batch, causal, schedule, stream);
+    launch_fused<128, WAVES, MASK, false>(a, batch, causal, schedule, stream);
   else
-    launch_fused<64, WAVES, MASK>(a, batch, causal, schedule, stream);
+    launch_fused<64, WAVES, MASK, false>(a, batch, causal, schedule, stream);
 }
 
 }  // namespace
@@ -41,6 +41,10 @@ int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
     launch_waves<4, true>(a, batch, head_dim, causal, schedule, stream);
   else if (policy == 2)
     launch_waves<8, false>(a, batch, head_dim, causal, Schedule::kStatic, stream);
+  else if (use_key_split(a, batch, head_dim, causal, policy) && head_dim == 128)
+    launch_fused<128, 8, false, true>(a, batch, causal, Schedule::kStatic, stream);
+  else if (use_key_split(a, batch, head_dim, causal, policy))
+    launch_fused<64, 8, false, true>(a, batch, causal, Schedule::kStatic, stream);
   else
     launch_waves<4, false>(a, batch, head_dim, causal, schedule, stream);
   return 0;
@@ -88,7 +92,25 @@ int64_t tile_steps_per_head(const FwdArgs& a, bool causal) {
 // neutral at N=8192, 2-5% slower for launches of short items).
 constexpr int64_t kDynamicMinSteps = 1024;
 
+// AUTO takes key-split workgroups at head_dim 128 for causal launches of at
+// most this many 128-row blocks per resident 128-row workgroup: every block
+// gets a slot at once, so the largest block's chain of key tiles sets the
+// launch time, and the split halves it.  Measured on MI355X (interleaved
+// A/B): B=1 Hq=8 N=8192 +14-16%, B=1 Hq=32 N=2048 +1%; with more blocks
+// than slots 5-13% slower; at head_dim 64 2-3% slower (its steps are bound
+// by the softmax arithmetic, not by the chain).
+constexpr int64_t kSplitMaxItems = 1;
+
 }  // namespace
+
+bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy) {
+  if (a.mbits != nullptr) return false;
+  if (policy == 4) return true;
+  if (policy != 0 || !causal || head_dim != 128) return false;
+  FwdArgs planned = a;
+  plan_grid(planned, batch, 128);
+  return planned.items <= kSplitMaxItems * resident_fused_workgroups();
+}
 
 bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedule schedule) {
   if (schedule == Schedule::kDynamic) return true;
@@ -99,7 +121,9 @@ bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedu
              kDynamicMinSteps * slots;
 }
 
-int64_t fused_workspace_bytes(const FwdArgs& a, int batch, bool causal, int policy) {
+int64_t fused_workspace_bytes(const FwdArgs& a, int batch, int head_dim, bool causal,
+                              int policy) {
+  if (use_key_split(a, batch, head_dim, causal, policy)) return 0;
   FwdArgs planned = a;
   plan_grid(planned, batch, 128);
   return use_dynamic_schedule(planned, batch, causal, schedule_of_policy(policy)) ? kTicketBytes

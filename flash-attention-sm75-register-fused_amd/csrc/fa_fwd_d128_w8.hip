@@ -2,5 +2,5 @@
 #include "fa_fwd_kernel.h"
 
 namespace fa {
-template void launch_fused<128, 8, false>(const FwdArgs&, int, bool, Schedule, hipStream_t);
+template void launch_fused<128, 8, false, false>(const FwdArgs&, int, bool, Schedule, hipStream_t);
 }  // namespace fa

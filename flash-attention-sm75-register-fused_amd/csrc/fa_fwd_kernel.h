@@ -68,11 +68,17 @@ namespace {
 //   * 8 waves, 256 query rows, one workgroup per CU, triple buffered
 //     (STAGES = 3): step j loads K_{j+3} and V_{j+2}, which have until the
 //     end of step j+1 to land; every K/V tile serves 256 query rows, and each
-//     wave issues half as many direct loads (waves 0-3 load K, 4-7 load V).
+//     wave issues half as many direct loads (waves 0-3 load K, 4-7 load V);
+//   * KSPLIT: 8 waves, 128 query rows, one workgroup per CU: waves w and w+4
+//     own the same 32 rows, and each group of 4 waves runs the 4-wave
+//     pipeline over its half of the block's key tiles in its own half of the
+//     LDS buffers; at the end group 1 hands its (O, max, sum) to group 0
+//     through LDS, which merges and stores.  This halves the longest chain
+//     of steps in launches whose time is set by their largest causal block.
 // KV_SAME_STRIDE: K and V rows have the same stride, so the direct-load
 // offsets are shared (saves registers).  MASK: an explicit mask (one 64-bit
 // word per query row and tile, loaded a step ahead) hides keys too.
-template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, bool MASK>
+template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, bool MASK, bool KSPLIT>
 __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
   using L = Lds<D>;
   constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
@@ -81,12 +87,14 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   constexpr int NPV = 4 * MT;      // P V MFMAs per tile
   constexpr int PFK = 3;           // K operand reads run this many MFMAs ahead
   constexpr int PFV = 2;           // V operand reads run this many MFMAs ahead
-  constexpr int BLOCK_M = 32 * WAVES;
-  constexpr int STAGES = WAVES == 8 ? 3 : 2;
-  constexpr int SEGQ = L::Segs / 4;           // segments of one tile per wave quarter
-  constexpr int LPW = 2 * L::Segs / WAVES;    // direct loads per wave per step
-  constexpr bool SPLIT_ROLES = WAVES == 8;    // a wave loads K or V, not both
+  constexpr int ROW_WAVES = KSPLIT ? 4 : WAVES;  // waves owning distinct rows
+  constexpr int BLOCK_M = 32 * ROW_WAVES;
+  constexpr int STAGES = WAVES == 8 && !KSPLIT ? 3 : 2;  // K/V buffers per tile kind
+  constexpr int SEGQ = L::Segs / 4;               // segments of one tile per wave quarter
+  constexpr int LPW = 2 * L::Segs / ROW_WAVES;    // direct loads per wave per step
+  constexpr bool SPLIT_ROLES = WAVES == 8 && !KSPLIT;  // a wave loads K or V, not both
   static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
+  static_assert(!KSPLIT || (WAVES == 8 && !MASK), "key split: 8 waves, no mask");
   static_assert(L::Segs % 4 == 0, "tile segments must split over 4 waves");
 
   // STAGES K buffers and STAGES V buffers, distinct objects (not one array):
@@ -94,16 +102,21 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   // compile time and the compiler can see that the in-flight direct loads
   // never alias the tiles being read (it would otherwise drain vmcnt before
   // each LDS read).
-  __shared__ __attribute__((aligned(1024))) _Float16 k_lds0[L::Tile];
-  __shared__ __attribute__((aligned(1024))) _Float16 k_lds1[L::Tile];
-  __shared__ __attribute__((aligned(1024))) _Float16 k_lds2[STAGES == 3 ? L::Tile : 1];
-  __shared__ __attribute__((aligned(1024))) _Float16 v_lds0[L::Tile];
-  __shared__ __attribute__((aligned(1024))) _Float16 v_lds1[L::Tile];
-  __shared__ __attribute__((aligned(1024))) _Float16 v_lds2[STAGES == 3 ? L::Tile : 1];
+  // With KSPLIT each array holds one tile per key group (group g at g Tile).
+  constexpr int GROUP_TILES = KSPLIT ? 2 : 1;
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds0[GROUP_TILES * L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds1[GROUP_TILES * L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds2[STAGES == 3 ? GROUP_TILES * L::Tile : 1];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds0[GROUP_TILES * L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds1[GROUP_TILES * L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds2[STAGES == 3 ? GROUP_TILES * L::Tile : 1];
 
   // Wave index: scalar (the direct loads' LDS destinations, M0, derive from
   // it) and the only thread coordinate kept across work items.
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int rw = KSPLIT ? wave & 3 : wave;     // row wave: rows q0 + 32 rw ..
+  const int kgrp = KSPLIT ? wave >> 2 : 0;     // key group (KSPLIT)
+  const int gofs = kgrp * L::Tile;             // its LDS tiles' offset
 
   // Work items.  Static schedule (a.ctr == nullptr): workgroup wg does item
   // wg.  Dynamic schedule (4-wave kernel, a.ctr set, grid = resident
@@ -119,14 +132,14 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   // claim raises h + t by one, so no item is claimed twice.
   // Thread 0 (wave 0, lane 0) claims the items (the head claim for the next
   // item is issued at the start of the item's last step) and passes the item
-  // and the set of queues it found empty to every wave through LDS: V_1's
-  // buffer, which no direct load writes between an item's last step and the
-  // next item's step 0.
+  // and the set of queues it found empty to every wave through LDS: the
+  // buffer of V_{STAGES-1}, which no direct load writes between an item's
+  // last step and the next item's step 0 (the prologue fills the others).
   const bool dynamic = WAVES == 4 && a.ctr != nullptr;
   const int nq = a.xcds;
   const int per_queue = a.items / nq;
   const int own_q = (int)(__builtin_amdgcn_s_getreg(kHwRegXccId) & 15u) % nq;
-  int* const ticket_slot = (int*)v_lds1;
+  int* const ticket_slot = (int*)(STAGES == 3 ? v_lds2 : v_lds1);
   auto lane_id = [] {
     return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   };
@@ -180,6 +193,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     const int tid = wave * 64 + lane;
     const int wq = wave & 3;    // quarter of the direct-load segments
     const bool v_role = SPLIT_ROLES && wave >= 4;
+
     const int hi = lane >> 5;   // which half of the wave
     const int ql = lane & 31;   // query column owned by this lane
     const int grp = lane >> 4;  // 16-lane group (transposing reads)
@@ -193,7 +207,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     const int b = w.b, hq = w.hq, hkv = w.hkv, qb = w.qb;
     const int bh = b * a.hq + hq;
     const int q0 = qb * BLOCK_M;
-    const int qw = q0 + wave * 32;
+    const int qw = q0 + rw * 32;
     const int qrow = qw + ql;
     const int N = a.n;    // query rows
     const int NK = a.nk;  // key rows
@@ -222,7 +236,13 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
 
     // Keys this block can see (none for a block entirely before the diagonal).
     const int kv_len = CAUSAL ? max(0, min(NK, q0 + BLOCK_M + a.diag)) : NK;
-    const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
+    const int block_tiles = (kv_len + kBlockN - 1) / kBlockN;
+    // Tiles [tile0, tile0 + ntiles) of this wave's key group.  KSPLIT: both
+    // groups run ceil(block_tiles / 2) steps (so their barriers pair up); a
+    // tile past the block's keys is fully masked and adds exactly nothing.
+    const int ntiles = KSPLIT ? (block_tiles + 1) / 2 : block_tiles;
+    const int tile0 = KSPLIT ? kgrp * ntiles : 0;
+    const int tile_end = tile0 + ntiles;
 
     // Direct-load map: wave quarter wq fills 1 KB segments wq, wq + 4, ... of a
     // tile; lane l of a segment covers tile bytes [1024 seg + 16 l, +16).  The
@@ -252,18 +272,18 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     const int k_all_bytes = (int)(NK * a.ksn * 2);
     const int v_all_bytes = (int)(NK * a.vsn * 2);
 
-    // Buffer selection by compile-time stage index.
+    // Buffer selection by compile-time stage index (and the key group).
     auto kbuf = [&](auto st) -> _Float16* {
       constexpr int S = decltype(st)::value % STAGES;
-      if constexpr (S == 0) return k_lds0;
-      else if constexpr (S == 1) return k_lds1;
-      else return k_lds2;
+      if constexpr (S == 0) return k_lds0 + gofs;
+      else if constexpr (S == 1) return k_lds1 + gofs;
+      else return k_lds2 + gofs;
     };
     auto vbuf = [&](auto st) -> _Float16* {
       constexpr int S = decltype(st)::value % STAGES;
-      if constexpr (S == 0) return v_lds0;
-      else if constexpr (S == 1) return v_lds1;
-      else return v_lds2;
+      if constexpr (S == 0) return v_lds0 + gofs;
+      else if constexpr (S == 1) return v_lds1 + gofs;
+      else return v_lds2 + gofs;
     };
     auto lds_seg = [&](_Float16* tile, int s) -> lds_void* {
       return (lds_void*)(tile + (wq + 4 * s) * 512);
@@ -507,33 +527,35 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     };
 
     // ---- prologue: K_0..K_{STAGES-1} and V_0..V_{STAGES-2} into LDS; S_0 -----
+    // (tile indices relative to tile0)
     if (ntiles > 0) {
       static_for<STAGES>([&](auto t_c) {
-        if (!v_role) load_tile(false, decltype(t_c)::value, kbuf(t_c));
+        if (!v_role) load_tile(false, tile0 + decltype(t_c)::value, kbuf(t_c));
       });
       static_for<STAGES - 1>([&](auto t_c) {
-        if (!SPLIT_ROLES || v_role) load_tile(true, decltype(t_c)::value, vbuf(t_c));
+        if (!SPLIT_ROLES || v_role) load_tile(true, tile0 + decltype(t_c)::value, vbuf(t_c));
       });
     }
     barrier_after_loads<0>();
     if (ntiles > 0) {
+      const _Float16* k_first = kbuf(std::integral_constant<int, 0>{});
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         s_buf[0][t] = (float16v)0.0f;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk)
-          s_buf[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(k_lds0, t * KK + kk), qf[kk],
-                                                               s_buf[0][t], 0, 0, 0);
+          s_buf[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(k_first, t * KK + kk),
+                                                               qf[kk], s_buf[0][t], 0, 0, 0);
       }
-      prepare(0, s_buf[0], halves_max(row_max(s_buf[0])), MASK ? mrow[0] : ~0ull);
+      prepare(tile0, s_buf[0], halves_max(row_max(s_buf[0])), MASK ? mrow[tile0] : ~0ull);
       // Step 0 loads K_STAGES into K_0's buffer: every wave must be done
       // reading it for S_0 first.
       __syncthreads();
       using I0 = std::integral_constant<int, 0>;
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;
-      int j = 0;
-      for (; j + STAGES < ntiles; j += STAGES) {  // every step has a next tile
+      int j = tile0;
+      for (; j + STAGES < tile_end; j += STAGES) {  // every step has a next tile
         step(j, Flag<true>{}, I0{});
         step(j + 1, Flag<true>{}, I1{});
         if constexpr (STAGES == 3) {
@@ -542,7 +564,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
           s_buf[0][1] = s_buf[1][1];
         }
       }
-      const int rest = ntiles - j;  // 1 .. STAGES steps left, the last one without a next tile
+      const int rest = tile_end - j;  // 1 .. STAGES steps left, the last one without a next tile
       if (rest == 1) {
         step(j, Flag<false>{}, I0{});
       } else if (STAGES == 2 || rest == 2) {
@@ -557,10 +579,54 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // No direct load may land in LDS after the workgroup ends.
     __builtin_amdgcn_s_waitcnt(0x0F70);
 
+    if constexpr (KSPLIT) {
+      // Group 1 wave w+4 hands its O (unnormalised), running max and partial
+      // sums to group 0 wave w (same rows, same lane layout) through the
+      // group-1 half of one LDS array, which no wave reads any more.
+      __syncthreads();
+      _Float16* const arr = rw == 0 ? k_lds0 : rw == 1 ? k_lds1 : rw == 2 ? v_lds0 : v_lds1;
+      float* const xo = (float*)(arr + L::Tile);
+      static_assert(MT * 16 * 64 * 4 + 2 * 64 * 4 <= L::Tile * 2, "exchange fits a tile");
+      if (kgrp == 1) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *(float4*)(xo + ((mt * 4 + g) * 64 + lane) * 4) =
+                float4{oacc[mt][4 * g], oacc[mt][4 * g + 1], oacc[mt][4 * g + 2],
+                       oacc[mt][4 * g + 3]};
+        xo[MT * 1024 + lane] = m_run;
+        xo[MT * 1024 + 64 + lane] = l_run;
+      }
+      __syncthreads();
+      if (kgrp == 0) {
+        const float m1 = xo[MT * 1024 + lane];
+        const float l1 = xo[MT * 1024 + 64 + lane];
+        const float m_new = fmaxf(m_run, m1);
+        const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
+        const float a0 =
+            (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * c2);
+        const float a1 =
+            (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m1 - m_use) * c2);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float4 o1 = *(const float4*)(xo + ((mt * 4 + g) * 64 + lane) * 4);
+            oacc[mt][4 * g] = oacc[mt][4 * g] * a0 + o1.x * a1;
+            oacc[mt][4 * g + 1] = oacc[mt][4 * g + 1] * a0 + o1.y * a1;
+            oacc[mt][4 * g + 2] = oacc[mt][4 * g + 2] * a0 + o1.z * a1;
+            oacc[mt][4 * g + 3] = oacc[mt][4 * g + 3] * a0 + o1.w * a1;
+          }
+        l_run = l_run * a0 + l1 * a1;
+        m_run = m_new;
+      }
+    }
+
     // ---- epilogue: combine the two half-wave partial sums, normalise, store ---
     const float l_tot = halves_sum(l_run);
     const float inv = (l_tot > 0.0f) ? (1.0f / l_tot) : 0.0f;
-    if (qrow < N) {
+    if (qrow < N && kgrp == 0) {
       _Float16* op = a.o + b * a.osb + hq * a.osh + (int64_t)qrow * a.osn;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -590,17 +656,17 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
 
 }  // namespace
 
-// Launches fa_fwd_kernel<D, ...> for one workgroup shape and mask mode; the
-// causal flag and K/V stride equality pick the instance.
+// Launches fa_fwd_kernel<D, ...> for one workgroup shape (WAVES, KSPLIT) and
+// mask mode; the causal flag and K/V stride equality pick the instance.
 // The dynamic schedule (use_dynamic_schedule) needs ticket counters in
 // a.ctr; they are cleared first, and the grid is one workgroup per resident
 // slot.
-template <int D, int WAVES, bool MASK>
+template <int D, int WAVES, bool MASK, bool KSPLIT>
 void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream) {
   const bool same = a.ksn == a.vsn;
   FwdArgs args = a;
-  int64_t wgs = plan_grid(args, batch, 32 * WAVES);
+  int64_t wgs = plan_grid(args, batch, KSPLIT ? 128 : 32 * WAVES);
   if (WAVES == 4 && args.ctr != nullptr && use_dynamic_schedule(args, batch, causal, schedule)) {
     launch_clear_tickets(args.ctr, stream);
     wgs = std::min<int64_t>(wgs, resident_fused_workgroups());
@@ -610,7 +676,7 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
   const dim3 grid((unsigned)wgs);
   const dim3 block(64 * WAVES);
 #define FA_LAUNCH(C, S) \
-  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK>), grid, block, 0, stream, args)
+  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK, KSPLIT>), grid, block, 0, stream, args)
   if (causal) {
     if (same) FA_LAUNCH(true, true); else FA_LAUNCH(true, false);
   } else {

@@ -52,7 +52,8 @@ void launch_clear_tickets(uint64_t* ctr, hipStream_t stream);
 // policy (fa_kernel_policy): 0 = automatic, 1 = 128-row workgroups of 4
 // waves (two per CU) on the static schedule, 2 = 256-row workgroups of 8
 // waves (one per CU, K/V triple-buffered), 3 = 128-row workgroups on the
-// dynamic schedule (when a.ctr is set).
+// dynamic schedule (when a.ctr is set), 4 = 128-row workgroups of 8 waves
+// splitting the keys (one per CU).
 int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
                          int policy, hipStream_t stream);
 // Schedules of the 4-wave kernel: the long-launch rule, or forced.
@@ -76,12 +77,17 @@ inline int64_t plan_grid(FwdArgs& a, int batch, int block_m) {
 bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedule schedule);
 // Workspace bytes the fused path uses for a call (the dynamic schedule's
 // counters, or 0), under a kernel policy.
-int64_t fused_workspace_bytes(const FwdArgs& a, int batch, bool causal, int policy);
+int64_t fused_workspace_bytes(const FwdArgs& a, int batch, int head_dim, bool causal,
+                              int policy);
 // One instance family of the fused kernel (fa_fwd_kernel.h), explicitly
-// instantiated in fa_fwd_d{64,128}{,_w8,_mask}.hip.
-template <int D, int WAVES, bool MASK>
+// instantiated in fa_fwd_d*.hip.  KSPLIT: 8 waves on 128 rows, the two
+// groups of 4 splitting the key tiles.
+template <int D, int WAVES, bool MASK, bool KSPLIT>
 void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream);
+// Whether a call runs on key-split workgroups: policy 4, or AUTO for causal
+// head_dim-128 launches whose time is set by their largest query block.
+bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy);
 int fused_block_m();  // rows of the smallest workgroup (grid-size checks)
 
 // Split-K path for few query rows per K/V head (fa_decode.hip): taken when

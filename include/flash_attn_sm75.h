@@ -141,20 +141,24 @@ const char* fa_sm75_status_string(int status);
 int fa_sm75_abi_version(void);
 
 /* Fused-kernel selection, process-wide (no reference counterpart: a tuning
- * and testing control).  AUTO picks by problem size (the split-K path for
- * few query rows per K/V head, else 128-row workgroups, with the dynamic
- * XCD-balanced schedule for long launches when p->workspace holds its
- * counters); NARROW forces 128-row workgroups of 4 waves (two workgroups per
- * CU) on the static schedule (one workgroup per query block); WIDE forces
- * 256-row workgroups of 8 waves (one per CU, K/V tiles triple-buffered);
- * DYNAMIC forces 128-row workgroups on the dynamic schedule whenever the
- * workspace holds its counters.  All compute the same function (the
+ * and testing control).  AUTO picks by problem size: the split-K path for
+ * few query rows per K/V head; key-split workgroups for causal head_dim-128
+ * launches small enough that their largest query block sets their time;
+ * else 128-row workgroups, with the dynamic XCD-balanced schedule for long
+ * launches when p->workspace holds its counters.  NARROW forces 128-row
+ * workgroups of 4 waves (two per CU) on the static schedule (one workgroup
+ * per query block); WIDE forces 256-row workgroups of 8 waves (one per CU,
+ * K/V tiles triple-buffered); DYNAMIC forces 128-row workgroups on the
+ * dynamic schedule whenever the workspace holds its counters; SPLIT forces
+ * 128-row workgroups of 8 waves, two groups of 4 each taking half of the
+ * block's key tiles (one per CU).  All compute the same function (the two
  * schedules bitwise so). */
 enum fa_kernel_policy {
   FA_POLICY_AUTO = 0,
   FA_POLICY_NARROW = 1,
   FA_POLICY_WIDE = 2,
-  FA_POLICY_DYNAMIC = 3
+  FA_POLICY_DYNAMIC = 3,
+  FA_POLICY_SPLIT = 4
 };
 int fa_sm75_set_kernel_policy(int policy); /* FA_OK or FA_ERR_INVALID_ARGUMENT */
 int fa_sm75_get_kernel_policy(void);

@@ -1,10 +1,13 @@
-"""Both fused kernel shapes against the oracle on the same inputs (needs a GPU).
+"""The fused kernel shapes against the oracle on the same inputs (needs a GPU).
 
 The prefill kernel comes as 128-row workgroups of 4 waves (two per CU, K/V
-double-buffered; the automatic choice) and 256-row workgroups of 8 waves (one
-per CU, K/V triple-buffered); fa_sm75_set_kernel_policy forces either, so
-each is checked on the same shapes, including the tails and 1-row cases the
-split-K path would otherwise take.  Tolerance as in test_gpu_parity:
+double-buffered; the automatic choice for most launches), 256-row workgroups
+of 8 waves (one per CU, K/V triple-buffered) and 128-row workgroups of 8
+waves whose two groups of 4 split the block's key tiles and merge through LDS
+(one per CU; the automatic choice for small causal launches);
+fa_sm75_set_kernel_policy forces each, so each is checked on the same shapes,
+including the tails, odd tile counts and 1-row cases the split-K path would
+otherwise take.  Tolerance as in test_gpu_parity:
 |O - O_ref| <= 2e-3 + 1e-2 |O_ref|.
 """
 import contextlib
@@ -20,7 +23,7 @@ from oracle import attention_ref as ref
 
 pytestmark = pytest.mark.gpu
 
-NARROW, WIDE = 1, 2
+NARROW, WIDE, SPLIT = 1, 2, 4
 
 
 @contextlib.contextmanager
@@ -63,10 +66,14 @@ SHAPES = [
     (1, 2, 2, 300, 64, True),
     (2, 4, 2, 777, 64, False),
     (1, 8, 8, 1100, 64, True),
+    (3, 5, 1, 129, 64, False),
+    (1, 2, 2, 65, 64, True),
+    (1, 2, 2, 130, 128, False),      # 3 key tiles: odd split
+    (4, 8, 8, 2048, 64, True),       # C3
 ]
 
 
-@pytest.mark.parametrize("pol", [NARROW, WIDE], ids=["narrow", "wide"])
+@pytest.mark.parametrize("pol", [NARROW, WIDE, SPLIT], ids=["narrow", "wide", "split"])
 @pytest.mark.parametrize("B,Hq,Hkv,N,D,causal", SHAPES)
 def test_forced_policy(device, pol, B, Hq, Hkv, N, D, causal):
     print(f"[policy {pol}] B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal}", flush=True)
@@ -77,10 +84,11 @@ def test_forced_policy(device, pol, B, Hq, Hkv, N, D, causal):
     check(out, q, k, v, causal, label=f"pol{pol} N{N} D{D}")
 
 
-@pytest.mark.parametrize("pol", [NARROW, WIDE], ids=["narrow", "wide"])
+@pytest.mark.parametrize("pol", [NARROW, WIDE, SPLIT], ids=["narrow", "wide", "split"])
 @pytest.mark.parametrize("scale", [0.0, -0.1, 1.0])
-def test_forced_policy_scales_and_lse(device, pol, scale):
-    q, k, v = inputs(1, 4, 2, 333, 128, seed=5)
+@pytest.mark.parametrize("D", [64, 128])
+def test_forced_policy_scales_and_lse(device, pol, scale, D):
+    q, k, v = inputs(1, 4, 2, 333, D, seed=5)
     with policy(pol):
         out, lse = flash_attention_forward_lse(q.to(device), k.to(device), v.to(device),
                                                causal=True, scale=scale)
@@ -90,17 +98,34 @@ def test_forced_policy_scales_and_lse(device, pol, scale):
     np.testing.assert_allclose(lse.cpu().numpy(), lse_ref, atol=2e-4, rtol=1e-5)
 
 
-def test_kernels_agree_and_auto_picks_one(device):
-    """Auto mode equals one of the forced kernels bit for bit, on a size the
-    automatic choice sends to the wide kernel and on one it sends to the
-    narrow kernel."""
-    for (B, Hq, Hkv, N) in ((4, 32, 8, 1000), (1, 4, 4, 300)):
-        q, k, v = (t.to(device) for t in inputs(B, Hq, Hkv, N, 128, seed=B * N))
+def test_key_split_auto_picks_one(device):
+    """The automatic choice equals a forced kernel bit for bit: key-split
+    workgroups on small causal launches at head_dim 128, 128-row ones
+    otherwise; the two kernels differ only by the merge's rounding."""
+    for (B, Hq, Hkv, N, D) in ((1, 8, 8, 2100, 128), (4, 8, 8, 2048, 64), (2, 32, 8, 2048, 128)):
+        q, k, v = (t.to(device) for t in inputs(B, Hq, Hkv, N, D, seed=B + N + D))
         outs = {}
-        for pol in (0, NARROW, WIDE):
+        for pol in (0, NARROW, SPLIT):
             with policy(pol):
                 outs[pol] = flash_attention_forward(q, k, v, causal=True)
         torch.cuda.synchronize()
-        assert torch.equal(outs[0], outs[NARROW]) or torch.equal(outs[0], outs[WIDE])
-        diff = (outs[NARROW].float() - outs[WIDE].float()).abs().max().item()
+        assert torch.equal(outs[0], outs[NARROW]) or torch.equal(outs[0], outs[SPLIT])
+        diff = (outs[NARROW].float() - outs[SPLIT].float()).abs().max().item()
         assert diff < 4e-3, diff
+
+
+def test_kernels_agree_and_auto_picks_one(device):
+    """Auto mode equals one of the forced kernels bit for bit, on a large
+    causal launch (128-row kernel) and a small one (key-split kernel); the
+    forced kernels agree within rounding."""
+    for (B, Hq, Hkv, N) in ((4, 32, 8, 1000), (1, 4, 4, 300)):
+        q, k, v = (t.to(device) for t in inputs(B, Hq, Hkv, N, 128, seed=B * N))
+        outs = {}
+        for pol in (0, NARROW, WIDE, SPLIT):
+            with policy(pol):
+                outs[pol] = flash_attention_forward(q, k, v, causal=True)
+        torch.cuda.synchronize()
+        assert any(torch.equal(outs[0], outs[p]) for p in (NARROW, WIDE, SPLIT))
+        for p in (WIDE, SPLIT):
+            diff = (outs[NARROW].float() - outs[p].float()).abs().max().item()
+            assert diff < 4e-3, (p, diff)
