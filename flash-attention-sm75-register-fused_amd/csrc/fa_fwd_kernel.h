@@ -469,6 +469,11 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         pf[2 * t + (i >> 3)][i & 7] = pr[0];
         pf[2 * t + (i >> 3)][(i & 7) + 1] = pr[1];
         l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
+        // Keeps the row-sum update in this slot: left alone, the compiler
+        // sinks all 16 of a step's (serially dependent) updates, with
+        // repacks of their operands, to after the last MFMA, where nothing
+        // hides their latency.
+        asm volatile("" : "+v"(l_run));
       };
       static_for<16>([&](auto p_c) {
         if constexpr (pair_slot(decltype(p_c)::value) < 0) softmax_pair(p_c);
