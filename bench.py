@@ -1,7 +1,8 @@
 """Benchmark of the fused attention forward on one MI355X.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
-                  [--no-cpu-baseline] [--all] [--decode] [--hf]
+                  [--no-cpu-baseline] [--no-gemm-ceiling] [--all] [--decode] [--hf]
+                  [--shape B,Hq,Hkv,N,D,causal]
 
 A step is one fused forward over one batch of synthetic input (the hot path:
 flash_attention_sm75.flash_attention_forward -> flash_attn_sm75_cuda ->
@@ -312,6 +313,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C4", choices=sorted(CONFIGS))
+    ap.add_argument("--shape", default=None,
+                    help="diagnostic: time B,Hq,Hkv,N,D,causal (N(0,1) data) instead of a "
+                         "BASELINE config, e.g. 1,8,8,8192,128,1")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemm-ceiling", action="store_true",
                     help="skip the fp16 GEMM run that measures the sustained MFMA rate")
@@ -342,6 +346,12 @@ def main():
     import torch
 
     cfg = args.config
+    if args.shape:
+        b_, hq_, hkv_, n_, d_, c_ = (int(x) for x in args.shape.split(","))
+        cfg = "custom"
+        CONFIGS[cfg] = (b_, hq_, hkv_, n_, d_, bool(c_), 1.0, False)
+        DESCR[cfg] = (f"{'causal' if c_ else 'full'} attention fwd B={b_} Hq={hq_} Hkv={hkv_} "
+                      f"N={n_} d={d_} (diagnostic shape)")
     B, Hq, Hkv, N, D, causal, _, _ = CONFIGS[cfg]
     if args.policy:
         import flash_attn_sm75_cuda as _C
