@@ -37,6 +37,8 @@ EXT_NAME = "flash_attn_sm75_cuda"
 HIP_SOURCES = [
     "fa_fwd_d128.hip", "fa_fwd_d128_mask.hip", "fa_fwd_d128_w8.hip", "fa_fwd_d128_ks.hip",
     "fa_fwd_d64.hip", "fa_fwd_d64_mask.hip", "fa_fwd_d64_w8.hip", "fa_fwd_d64_ks.hip",
+    "fa_fwd_d128_bf16.hip", "fa_fwd_d128_mask_bf16.hip", "fa_fwd_d128_ks_bf16.hip",
+    "fa_fwd_d64_bf16.hip", "fa_fwd_d64_mask_bf16.hip", "fa_fwd_d64_ks_bf16.hip",
     "fa_fwd.hip", "fa_decode.hip", "fa_mask.hip", "fa_naive.hip", "fa_capi.hip",
 ]
 

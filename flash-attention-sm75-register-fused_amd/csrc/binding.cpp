@@ -8,8 +8,8 @@
 // Additions: flash_attention_forward accepts grouped K/V heads (Hkv divides
 // Hq) so no repeat_interleave copy is needed, flash_attention_forward_lse
 // also returns the fp32 row log-sum-exp, and flash_attention_forward_ex takes
-// strided views in place, Nq != Nk, either causal alignment and a boolean
-// attn_mask.
+// strided views in place, Nq != Nk, either causal alignment, a boolean
+// attn_mask and bfloat16 tensors (the reference ops stay FP16 only).
 //
 // All checks run before any device work; the kernels are enqueued on the
 // current HIP stream of Q's device and the host is not blocked.
@@ -38,14 +38,22 @@ void check_same_device(const torch::Tensor& Q, const torch::Tensor& K,
               "Q, K, V must be on the same device");
 }
 
+// Data pointers and element type of 16-bit tensors (binary16 or bfloat16,
+// checked by the callers).
+void set_tensors(fa_fwd_params& p, const torch::Tensor& Q, const torch::Tensor& K,
+                 const torch::Tensor& V, torch::Tensor& O) {
+  p.q = static_cast<const fa_half*>(Q.data_ptr());
+  p.k = static_cast<const fa_half*>(K.data_ptr());
+  p.v = static_cast<const fa_half*>(V.data_ptr());
+  p.o = static_cast<fa_half*>(O.data_ptr());
+  p.dtype = Q.scalar_type() == torch::kBFloat16 ? FA_DTYPE_BF16 : FA_DTYPE_FP16;
+}
+
 fa_fwd_params make_params(const torch::Tensor& Q, const torch::Tensor& K,
                           const torch::Tensor& V, torch::Tensor& O, float* lse,
                           bool causal, float scale) {
   fa_fwd_params p{};
-  p.q = reinterpret_cast<const fa_half*>(Q.data_ptr<at::Half>());
-  p.k = reinterpret_cast<const fa_half*>(K.data_ptr<at::Half>());
-  p.v = reinterpret_cast<const fa_half*>(V.data_ptr<at::Half>());
-  p.o = reinterpret_cast<fa_half*>(O.data_ptr<at::Half>());
+  set_tensors(p, Q, K, V, O);
   p.lse = lse;
   p.batch = Q.size(0);
   p.heads_q = Q.size(1);
@@ -183,7 +191,9 @@ std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_
   for (auto* pr : {&Q, &K, &V}) {
     const torch::Tensor& t = *pr;
     TORCH_CHECK(t.is_cuda(), "inputs must be CUDA tensors");
-    TORCH_CHECK(t.dtype() == torch::kFloat16, "inputs must be FP16");
+    TORCH_CHECK(t.dtype() == torch::kFloat16 || t.dtype() == torch::kBFloat16,
+                "inputs must be FP16 or BF16");
+    TORCH_CHECK(t.dtype() == Q.dtype(), "Q, K and V must have the same dtype");
     TORCH_CHECK(t.dim() == 4, "inputs must be [B, H, N, D]");
   }
   check_same_device(Q, K, V);
@@ -208,10 +218,7 @@ std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_
   TORCH_CHECK(K.size(2) > 0, "K/V must hold at least one row");
   const at::OptionalDeviceGuard guard(at::device_of(Q));
   fa_fwd_params p{};
-  p.q = reinterpret_cast<const fa_half*>(Q.data_ptr<at::Half>());
-  p.k = reinterpret_cast<const fa_half*>(K.data_ptr<at::Half>());
-  p.v = reinterpret_cast<const fa_half*>(V.data_ptr<at::Half>());
-  p.o = reinterpret_cast<fa_half*>(O.data_ptr<at::Half>());
+  set_tensors(p, Q, K, V, O);
   p.lse = return_lse ? L->data_ptr<float>() : nullptr;
   p.batch = Q.size(0);
   p.heads_q = Q.size(1);

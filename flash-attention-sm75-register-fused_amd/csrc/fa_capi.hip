@@ -71,6 +71,11 @@ int validate(const fa_fwd_params* p, bool fused) {
                 p->causal);
   if (!fused && p->seq_len_kv != 0 && p->seq_len_kv != p->seq_len)
     return fail(FA_ERR_INVALID_ARGUMENT, "naive path needs seq_len_kv == seq_len");
+  if (p->dtype != FA_DTYPE_FP16 && p->dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_INVALID_ARGUMENT, "dtype must be 0 (binary16) or 1 (bfloat16), got %d",
+                p->dtype);
+  if (!fused && p->dtype != FA_DTYPE_FP16)
+    return fail(FA_ERR_INVALID_ARGUMENT, "the naive path is binary16 only");
   const bool empty = p->batch == 0 || p->heads_q == 0 || p->seq_len == 0;
   if (empty) return FA_OK;
   if (!p->q || !p->k || !p->v || !p->o)
@@ -158,6 +163,7 @@ fa::FwdArgs make_args(const fa_fwd_params* p) {
   a.msq = p->mask_stride_q;
   a.ctr = nullptr;
   a.items = 0;
+  a.bf16 = p->dtype == FA_DTYPE_BF16 ? 1 : 0;
   return a;
 }
 

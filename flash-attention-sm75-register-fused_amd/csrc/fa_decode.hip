@@ -61,10 +61,11 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
-template <int D, bool CAUSAL, bool MASK>
+template <int D, bool CAUSAL, bool MASK, bool BF16>
 __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d) {
   const FwdArgs& a = d.f;
   using L = DecLds<D>;
+  using E = Elem<BF16>;
   constexpr int KK = D / 16;   // 16-wide contraction steps of S^T
   constexpr int MT = D / 32;   // 32-row output tiles of O^T
   constexpr int NPV = 2 * MT;  // P V MFMAs per 32-key tile
@@ -110,7 +111,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   }
   if (a.negate_q) {
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) qf[kk] = -qf[kk];
+    for (int kk = 0; kk < KK; ++kk) qf[kk] = negate16(qf[kk]);
   }
 
   // Tiles of this split, and this wave's share (every fourth one).
@@ -202,7 +203,6 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   float m_run = -__builtin_inff();
   float l_run = 0.0f;
   const float c2 = a.c;
-  const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
   const int diag_row = qi + a.diag;  // causal: keys <= diag_row are visible
 
   half8 kA[KK], kB[KK];
@@ -217,7 +217,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     float16v s = (float16v)0.0f;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kc[kk], qf[kk], s, 0, 0, 0);
+      s = E::mfma(kc[kk], qf[kk], s);
 
     const int kstart = key0 + (wave + kWaves * it) * kDecTile;
     bool need_mask = (kstart + kDecTile > NK) || (CAUSAL && kstart + kDecTile - 1 > a.diag);
@@ -253,10 +253,10 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     for (int i = 0; i < 16; i += 2) {
       const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c2, -mc));
       const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i + 1], c2, -mc));
-      const half2v pr = {(_Float16)p0, (_Float16)p1};
+      const half2v pr = E::pack(p0, p1);
       pf[i >> 3][i & 7] = pr[0];
       pf[i >> 3][(i & 7) + 1] = pr[1];
-      l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
+      l_run = E::sum2(pr, l_run);
     }
     // V of this tile has landed once only the next tile's loads are pending
     // (loads complete in order).
@@ -267,7 +267,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
 #pragma unroll
     for (int v = 0; v < NPV; ++v) {
       const int ks = v / MT, mt = v % MT;
-      oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[v], pf[ks], oacc[mt], 0, 0, 0);
+      oacc[mt] = E::mfma(vf[v], pf[ks], oacc[mt]);
     }
   };
 
@@ -335,7 +335,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     for (int g4 = 0; g4 < 4; ++g4) {
       half4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (_Float16)(o[4 * g4 + e] * inv);
+      for (int e = 0; e < 4; ++e) v[e] = E::round(o[4 * g4 + e] * inv);
       *(half4*)(op + 8 * g4) = v;
     }
     if (a.lse != nullptr && mt == 0 && hi == 0) {
@@ -367,7 +367,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
 constexpr int kCombineThreads = 256;
 constexpr int kMaxSplits = 1024;
 
-template <int D>
+template <int D, bool BF16>
 __global__ void __launch_bounds__(kCombineThreads) fa_decode_combine(const DecArgs d) {
   const FwdArgs& a = d.f;
   constexpr int GROUPS = kCombineThreads / D;
@@ -437,11 +437,37 @@ __global__ void __launch_bounds__(kCombineThreads) fa_decode_combine(const DecAr
 #pragma unroll
   for (int q = 0; q < GROUPS; ++q) o += o_part[q][dim];
   const float inv = (Ltot > 0.0f) ? (1.0f / Ltot) : 0.0f;
-  a.o[b * a.osb + hq * a.osh + (int64_t)qi * a.osn + dim] = (_Float16)(o * inv);
+  a.o[b * a.osb + hq * a.osh + (int64_t)qi * a.osn + dim] = Elem<BF16>::round(o * inv);
   if (a.lse != nullptr && dim == 0) {
     const float m_use = (M == -__builtin_inff()) ? 0.0f : M;
     a.lse[((int64_t)b * a.hq + hq) * a.n + qi] =
         (m_use + __builtin_log2f(Ltot)) * 0.69314718055994530942f;
+  }
+}
+
+template <bool BF16>
+void launch_decode_typed(const DecArgs& d, const DecodePlan& pl, int head_dim, bool causal,
+                         hipStream_t stream) {
+  const dim3 grid((unsigned)((int64_t)pl.units * pl.splits));
+#define FA_DEC(DD, C, M) \
+  hipLaunchKernelGGL((fa_decode_kernel<DD, C, M, BF16>), grid, dim3(kThreads), 0, stream, d)
+#define FA_DEC_M(DD, C) \
+  if (d.f.mbits != nullptr) FA_DEC(DD, C, true); else FA_DEC(DD, C, false)
+  if (head_dim == 128) {
+    if (causal) { FA_DEC_M(128, true); } else { FA_DEC_M(128, false); }
+  } else {
+    if (causal) { FA_DEC_M(64, true); } else { FA_DEC_M(64, false); }
+  }
+#undef FA_DEC_M
+#undef FA_DEC
+  if (pl.splits > 1) {
+    const dim3 cgrid((unsigned)((int64_t)pl.units * pl.rows));
+    if (head_dim == 128)
+      hipLaunchKernelGGL((fa_decode_combine<128, BF16>), cgrid, dim3(kCombineThreads), 0, stream,
+                         d);
+    else
+      hipLaunchKernelGGL((fa_decode_combine<64, BF16>), cgrid, dim3(kCombineThreads), 0, stream,
+                         d);
   }
 }
 
@@ -485,25 +511,10 @@ int launch_decode_forward(const FwdArgs& a, const DecodePlan& pl, int head_dim, 
   d.part_ml = pl.splits > 1
                   ? d.part_o + (int64_t)pl.units * pl.splits * pl.rows * head_dim
                   : nullptr;
-  const dim3 grid((unsigned)((int64_t)pl.units * pl.splits));
-#define FA_DEC(DD, C, M) \
-  hipLaunchKernelGGL((fa_decode_kernel<DD, C, M>), grid, dim3(kThreads), 0, stream, d)
-#define FA_DEC_M(DD, C) \
-  if (a.mbits != nullptr) FA_DEC(DD, C, true); else FA_DEC(DD, C, false)
-  if (head_dim == 128) {
-    if (causal) { FA_DEC_M(128, true); } else { FA_DEC_M(128, false); }
-  } else {
-    if (causal) { FA_DEC_M(64, true); } else { FA_DEC_M(64, false); }
-  }
-#undef FA_DEC_M
-#undef FA_DEC
-  if (pl.splits > 1) {
-    const dim3 cgrid((unsigned)((int64_t)pl.units * pl.rows));
-    if (head_dim == 128)
-      hipLaunchKernelGGL(fa_decode_combine<128>, cgrid, dim3(kCombineThreads), 0, stream, d);
-    else
-      hipLaunchKernelGGL(fa_decode_combine<64>, cgrid, dim3(kCombineThreads), 0, stream, d);
-  }
+  if (a.bf16)
+    launch_decode_typed<true>(d, pl, head_dim, causal, stream);
+  else
+    launch_decode_typed<false>(d, pl, head_dim, causal, stream);
   return 0;
 }
 

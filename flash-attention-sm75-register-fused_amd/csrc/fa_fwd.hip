@@ -1,7 +1,7 @@
 // Fused attention forward for gfx950 (MI355X / CDNA4): kernel selection.
 //
-// The kernel itself (fa_fwd_kernel.h) is instantiated per head dimension and
-// workgroup shape in fa_fwd_d*.hip, which compile in
+// The kernel itself (fa_fwd_kernel.h) is instantiated per head dimension,
+// workgroup shape and element type in fa_fwd_d*.hip, which compile in
 // parallel; this file picks the instance for a call.
 #include <hip/hip_runtime.h>
 
@@ -18,35 +18,43 @@ __global__ void fa_clear_tickets(uint64_t* ctr) {
   for (int i = threadIdx.x; i < kNumXcds; i += blockDim.x) ctr[i * kCtrStride] = 0ull;
 }
 
-template <int WAVES, bool MASK>
-void launch_waves(const FwdArgs& a, int batch, int head_dim, bool causal, Schedule schedule,
+template <int WAVES, bool MASK, bool KSPLIT, bool BF16>
+void launch_shape(const FwdArgs& a, int batch, int head_dim, bool causal, Schedule schedule,
                   hipStream_t stream) {
   if (head_dim == 128)
-    launch_fused<128, WAVES, MASK, false>(a, batch, causal, schedule, stream);
+    launch_fused<128, WAVES, MASK, KSPLIT, BF16>(a, batch, causal, schedule, stream);
   else
-    launch_fused<64, WAVES, MASK, false>(a, batch, causal, schedule, stream);
+    launch_fused<64, WAVES, MASK, KSPLIT, BF16>(a, batch, causal, schedule, stream);
 }
-
-}  // namespace
 
 // The 8-wave (256-row, one workgroup per CU) kernel only runs when asked
 // for (FA_POLICY_WIDE): measured on C4 it is ~4% slower than the 4-wave
 // kernel -- with one workgroup per CU both waves of a SIMD stop at the same
-// barrier, where two independent 4-wave workgroups cover each other's.
+// barrier, where two independent 4-wave workgroups cover each other's.  It
+// is built for binary16 only (bfloat16 calls take the 4-wave kernel).
 // Masked calls always take the 4-wave kernel.
-int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
-                         int policy, hipStream_t stream) {
+template <bool BF16>
+void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int policy,
+                  hipStream_t stream) {
   const Schedule schedule = schedule_of_policy(policy);
   if (a.mbits != nullptr)
-    launch_waves<4, true>(a, batch, head_dim, causal, schedule, stream);
-  else if (policy == 2)
-    launch_waves<8, false>(a, batch, head_dim, causal, Schedule::kStatic, stream);
-  else if (use_key_split(a, batch, head_dim, causal, policy) && head_dim == 128)
-    launch_fused<128, 8, false, true>(a, batch, causal, Schedule::kStatic, stream);
+    launch_shape<4, true, false, BF16>(a, batch, head_dim, causal, schedule, stream);
+  else if (policy == 2 && !BF16)
+    launch_shape<8, false, false, false>(a, batch, head_dim, causal, Schedule::kStatic, stream);
   else if (use_key_split(a, batch, head_dim, causal, policy))
-    launch_fused<64, 8, false, true>(a, batch, causal, Schedule::kStatic, stream);
+    launch_shape<8, false, true, BF16>(a, batch, head_dim, causal, Schedule::kStatic, stream);
   else
-    launch_waves<4, false>(a, batch, head_dim, causal, schedule, stream);
+    launch_shape<4, false, false, BF16>(a, batch, head_dim, causal, schedule, stream);
+}
+
+}  // namespace
+
+int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,
+                         int policy, hipStream_t stream) {
+  if (a.bf16)
+    launch_typed<true>(a, batch, head_dim, causal, policy, stream);
+  else
+    launch_typed<false>(a, batch, head_dim, causal, policy, stream);
   return 0;
 }
 

@@ -1,6 +1,7 @@
-// Fused forward instances: head_dim 128, 128-row workgroups of 8 waves splitting the keys.
+// Fused forward instances (binary16): head_dim 128, 128-row workgroups of 8 waves splitting the keys.
 #include "fa_fwd_kernel.h"
 
 namespace fa {
-template void launch_fused<128, 8, false, true>(const FwdArgs&, int, bool, Schedule, hipStream_t);
+template void launch_fused<128, 8, false, true, false>(const FwdArgs&, int, bool, Schedule,
+                                                      hipStream_t);
 }  // namespace fa

@@ -1,6 +1,7 @@
-// Fused forward instances: head_dim 128, 128-row workgroups (4 waves) with a boolean mask.
+// Fused forward instances (binary16): head_dim 128, 128-row workgroups (4 waves) with a boolean mask.
 #include "fa_fwd_kernel.h"
 
 namespace fa {
-template void launch_fused<128, 4, true, false>(const FwdArgs&, int, bool, Schedule, hipStream_t);
+template void launch_fused<128, 4, true, false, false>(const FwdArgs&, int, bool, Schedule,
+                                                      hipStream_t);
 }  // namespace fa

@@ -1,0 +1,7 @@
+// Fused forward instances (bfloat16): head_dim 128, 128-row workgroups (4 waves) with a boolean mask.
+#include "fa_fwd_kernel.h"
+
+namespace fa {
+template void launch_fused<128, 4, true, false, true>(const FwdArgs&, int, bool, Schedule,
+                                                      hipStream_t);
+}  // namespace fa

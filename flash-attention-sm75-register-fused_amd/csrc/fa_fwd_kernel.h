@@ -78,9 +78,10 @@ namespace {
 // KV_SAME_STRIDE: K and V rows have the same stride, so the direct-load
 // offsets are shared (saves registers).  MASK: an explicit mask (one 64-bit
 // word per query row and tile, loaded a step ahead) hides keys too.
-template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, bool MASK, bool KSPLIT>
+template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, bool MASK, bool KSPLIT, bool BF16>
 __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
   using L = Lds<D>;
+  using E = Elem<BF16>;
   constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
   constexpr int MT = D / 32;       // 32-row output tiles of O^T
   constexpr int NS = 2 * KK;       // S^T MFMAs per tile
@@ -231,7 +232,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     }
     if (a.negate_q) {
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) qf[kk] = -qf[kk];
+      for (int kk = 0; kk < KK; ++kk) qf[kk] = negate16(qf[kk]);
     }
 
     // Keys this block can see (none for a block entirely before the diagonal).
@@ -336,7 +337,6 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     float m_run = -__builtin_inff();
     float l_run = 0.0f;
     const float c2 = a.c;  // |scale| * log2(e)
-    const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 
     // S^T of two tiles in flight, ping-pong by the parity of the step's
     // position in the unrolled loop: step u reads s_buf[u & 1] and fills the
@@ -465,10 +465,10 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         constexpr int t = e >> 4, i = e & 15;
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i], c2, -mc));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i + 1], c2, -mc));
-        const half2v pr = {(_Float16)p0, (_Float16)p1};
+        const half2v pr = E::pack(p0, p1);
         pf[2 * t + (i >> 3)][i & 7] = pr[0];
         pf[2 * t + (i >> 3)][(i & 7) + 1] = pr[1];
-        l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
+        l_run = E::sum2(pr, l_run);
         // Keeps the row-sum update in this slot: left alone, the compiler
         // sinks all 16 of a step's (serially dependent) updates, with
         // repacks of their operands, to after the last MFMA, where nothing
@@ -498,12 +498,11 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
           constexpr int i = slot;
           if constexpr (i + PFK < ns) kf[i + PFK] = read_k(Kn, i + PFK);
           constexpr int t = i / KK, kk = i % KK;
-          s_nxt[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-              kf[i], qf[kk], kk == 0 ? (float16v)0.0f : s_nxt[t], 0, 0, 0);
+          s_nxt[t] = E::mfma(kf[i], qf[kk], kk == 0 ? (float16v)0.0f : s_nxt[t]);
         } else {
           constexpr int v = slot - PV_FIRST;
           constexpr int ks = v / MT, mt = v % MT;
-          oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[v], pf[ks], oacc[mt], 0, 0, 0);
+          oacc[mt] = E::mfma(vf[v], pf[ks], oacc[mt]);
         }
         if constexpr (HAS_NEXT) {
           static_for<LPW>([&](auto q_c) {
@@ -549,8 +548,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         s_buf[0][t] = (float16v)0.0f;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk)
-          s_buf[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(k_first, t * KK + kk),
-                                                               qf[kk], s_buf[0][t], 0, 0, 0);
+          s_buf[0][t] = E::mfma(read_k(k_first, t * KK + kk), qf[kk], s_buf[0][t]);
       }
       prepare(tile0, s_buf[0], halves_max(row_max(s_buf[0])), MASK ? mrow[tile0] : ~0ull);
       // Step 0 loads K_STAGES into K_0's buffer: every wave must be done
@@ -639,7 +637,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         for (int g = 0; g < 4; ++g) {
           half4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (_Float16)(oacc[mt][4 * g + e] * inv);
+          for (int e = 0; e < 4; ++e) v[e] = E::round(oacc[mt][4 * g + e] * inv);
           *(half4*)(op + 32 * mt + 8 * g + 4 * hi) = v;
         }
       }
@@ -666,7 +664,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
 // The dynamic schedule (use_dynamic_schedule) needs ticket counters in
 // a.ctr; they are cleared first, and the grid is one workgroup per resident
 // slot.
-template <int D, int WAVES, bool MASK, bool KSPLIT>
+template <int D, int WAVES, bool MASK, bool KSPLIT, bool BF16>
 void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream) {
   const bool same = a.ksn == a.vsn;
@@ -681,7 +679,8 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
   const dim3 grid((unsigned)wgs);
   const dim3 block(64 * WAVES);
 #define FA_LAUNCH(C, S) \
-  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK, KSPLIT>), grid, block, 0, stream, args)
+  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK, KSPLIT, BF16>), grid, block, 0, stream, \
+                     args)
   if (causal) {
     if (same) FA_LAUNCH(true, true); else FA_LAUNCH(true, false);
   } else {

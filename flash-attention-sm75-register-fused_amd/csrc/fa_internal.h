@@ -35,6 +35,7 @@ struct FwdArgs {
   int64_t msb, msh, msq;   // its strides in 64-bit words
   uint64_t* ctr;    // queue counters of the dynamic schedule, or nullptr (static)
   int items;        // work items (query blocks): filled by the launcher
+  int bf16;         // elements are bfloat16 (else binary16)
 };
 
 // Dynamic schedule of the fused kernel: one 64-bit (head, tail) counter per
@@ -82,7 +83,7 @@ int64_t fused_workspace_bytes(const FwdArgs& a, int batch, int head_dim, bool ca
 // One instance family of the fused kernel (fa_fwd_kernel.h), explicitly
 // instantiated in fa_fwd_d*.hip.  KSPLIT: 8 waves on 128 rows, the two
 // groups of 4 splitting the key tiles.
-template <int D, int WAVES, bool MASK, bool KSPLIT>
+template <int D, int WAVES, bool MASK, bool KSPLIT, bool BF16>
 void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream);
 // Whether a call runs on key-split workgroups: policy 4, or AUTO for causal

@@ -17,7 +17,55 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short short8v __attribute__((ext_vector_type(8)));
+
 typedef __attribute__((address_space(3))) void lds_void;
+
+// Element type of Q, K, V, O and P.  Every 16-bit value moves as a _Float16
+// container (global and direct loads, LDS, transposing reads); only the
+// MFMAs, the fp32 -> 16-bit roundings (round to nearest even) and the pair
+// sums of P interpret the bits.
+template <bool BF16>
+struct Elem;
+template <>
+struct Elem<false> {  // binary16
+  static __device__ __forceinline__ float16v mfma(half8 a, half8 b, float16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ half2v pack(float x, float y) {
+    return half2v{(_Float16)x, (_Float16)y};
+  }
+  // acc + x + y of a packed pair (one v_dot2 against (1, 1)).
+  static __device__ __forceinline__ float sum2(half2v p, float acc) {
+    const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(p, ones, acc, false);
+  }
+  static __device__ __forceinline__ _Float16 round(float x) { return (_Float16)x; }
+};
+template <>
+struct Elem<true> {  // bfloat16
+  static __device__ __forceinline__ float16v mfma(half8 a, half8 b, float16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ half2v pack(float x, float y) {
+    return __builtin_bit_cast(half2v, bf16x2{(__bf16)x, (__bf16)y});
+  }
+  static __device__ __forceinline__ float sum2(half2v p, float acc) {
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), ones, acc, false);
+  }
+  static __device__ __forceinline__ _Float16 round(float x) {
+    return __builtin_bit_cast(_Float16, (__bf16)x);
+  }
+};
+
+// -x of every element (sign flip; exact in either element type).
+__device__ __forceinline__ half8 negate16(half8 x) {
+  return __builtin_bit_cast(half8, __builtin_bit_cast(short8v, x) ^ (short8v)(short)0x8000);
+}
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;

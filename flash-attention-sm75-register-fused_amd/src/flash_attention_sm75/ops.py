@@ -127,11 +127,12 @@ def flash_attention_forward_ex(Q, K, V, causal=False, scale=None, return_lse=Fal
     contiguous tensors (reference pytorch_extension.cpp:22-25,61).
 
     Args:
-        Q: [B, H_q, N_q, D] float16 on the GPU; any layout whose head_dim is
-           contiguous and whose other strides are multiples of 8 is read in
-           place (e.g. a [B, N, H, D] buffer viewed as [B, H, N, D]), other
-           layouts are copied first.
-        K, V: [B, H_kv, N_k, D] float16, H_kv divides H_q.
+        Q: [B, H_q, N_q, D] float16 or bfloat16 on the GPU; any layout whose
+           head_dim is contiguous and whose other strides are multiples of 8
+           is read in place (e.g. a [B, N, H, D] buffer viewed as
+           [B, H, N, D]), other layouts are copied first.  With bfloat16 the
+           probabilities are rounded to bfloat16 before the P V product.
+        K, V: [B, H_kv, N_k, D], Q's dtype, H_kv divides H_q.
         causal: False; True or "top_left" (key j visible to query i iff
             j <= i, torch SDPA's is_causal); "bottom_right" (iff
             j <= i + N_k - N_q).  A query that sees no key gets a zero row.
@@ -142,8 +143,8 @@ def flash_attention_forward_ex(Q, K, V, causal=False, scale=None, return_lse=Fal
             packed to bits on the GPU and combines with ``causal``.
 
     Returns:
-        O [B, H_q, N_q, D] float16 with Q's memory layout when Q is dense,
-        or (O, LSE) when return_lse.
+        O [B, H_q, N_q, D] in Q's dtype with Q's memory layout when Q is
+        dense, or (O, LSE) when return_lse.
     """
     head_dim = _check_inputs(Q)
     if scale is None:

@@ -18,6 +18,8 @@ without changing results:
     viewed as [B, H, N, D]) and O keeps Q's layout, so the caller's
     ``transpose(1, 2).contiguous()`` is free;
   * grouped K/V heads go to the kernel as they are (no repeat_interleave);
+  * bfloat16 calls (most current models' dtype) run on the kernel's bfloat16
+    instances; other dtypes, and mixed ones, fall back;
   * calls that need gradients fall back (the kernel is forward-only).
 """
 import torch
@@ -45,8 +47,9 @@ def _fallback_reason(query, key, value, attn_mask, dropout_p, is_causal, kwargs)
     """Why a call cannot run on the kernel, or None (reference :47-64)."""
     if not query.is_cuda:
         return "not_cuda"
-    if query.dtype != torch.float16 or key.dtype != torch.float16 or value.dtype != torch.float16:
-        return "not_fp16"
+    if (query.dtype not in (torch.float16, torch.bfloat16) or key.dtype != query.dtype
+            or value.dtype != query.dtype):
+        return "not_fp16"  # the reference's name; bfloat16 runs on the kernel too
     if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
         return "not_4d"
     if query.size(-1) not in (64, 128):

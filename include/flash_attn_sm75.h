@@ -4,7 +4,8 @@
  * Plain pointers and sizes only: no torch, no HIP types in the signatures.
  * Every tensor is IEEE binary16 (`fa_half`, the bit pattern of CUDA's `half`)
  * laid out [batch, heads, seq_len, head_dim] with head_dim contiguous (K and V
- * may hold a different number of rows, seq_len_kv, in fa_sm75_forward).
+ * may hold a different number of rows, seq_len_kv, in fa_sm75_forward, which
+ * also takes bfloat16 tensors: fa_fwd_params.dtype).
  *
  * Two groups of entry points:
  *
@@ -34,8 +35,15 @@
 extern "C" {
 #endif
 
-/* One binary16 value (bit pattern). Only ever passed by pointer. */
+/* One 16-bit value (bit pattern): binary16, or bfloat16 where
+ * fa_fwd_params.dtype says so.  Only ever passed by pointer. */
 typedef uint16_t fa_half;
+
+/* Values of fa_fwd_params.dtype: the element type of Q, K, V and O.  No
+ * reference counterpart (the reference is binary16 only).  With bfloat16 the
+ * probabilities are rounded to bfloat16 before the P V product, as the
+ * binary16 path rounds them to binary16. */
+enum fa_dtype { FA_DTYPE_FP16 = 0, FA_DTYPE_BF16 = 1 };
 
 /* Status codes returned by fa_sm75_forward / fa_sm75_naive_forward. */
 enum fa_status {
@@ -97,6 +105,8 @@ typedef struct fa_fwd_params {
    * sees no key gets O = 0 and LSE = -inf. */
   const uint64_t* mask_bits;
   int64_t mask_stride_b, mask_stride_h, mask_stride_q;
+  int dtype;          /* an fa_dtype (0, binary16, in a zeroed struct); the
+                         naive path and the reference launchers are binary16 */
 } fa_fwd_params;
 
 /* Fills strides for contiguous [B,H,N,D] Q/O and [B,Hkv,Nk,D] K/V tensors. */
@@ -162,7 +172,7 @@ enum fa_kernel_policy {
 };
 int fa_sm75_set_kernel_policy(int policy); /* FA_OK or FA_ERR_INVALID_ARGUMENT */
 int fa_sm75_get_kernel_policy(void);
-#define FA_SM75_ABI_VERSION 2
+#define FA_SM75_ABI_VERSION 3
 
 /* ---- Reference launcher signatures ------------------------------------ */
 

@@ -22,7 +22,9 @@ class Params(ctypes.Structure):
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
         ("mask_bits", ctypes.c_void_p), ("mask_stride_b", ctypes.c_int64),
         ("mask_stride_h", ctypes.c_int64), ("mask_stride_q", ctypes.c_int64),
+        ("dtype", ctypes.c_int),
     ]]
 
 
 FA_CAUSAL_NONE, FA_CAUSAL_TOP_LEFT, FA_CAUSAL_BOTTOM_RIGHT = 0, 1, 2
+FA_DTYPE_FP16, FA_DTYPE_BF16 = 0, 1

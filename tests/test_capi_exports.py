@@ -103,6 +103,8 @@ def test_contiguous_strides_separate_kv_length(lib):
     (dict(seq_len_kv=1 << 30), 5, b"exceeds the supported maximum"),
     (dict(workspace=0x10004, workspace_bytes=64), 4, b"workspace must be 16-byte aligned"),
     (dict(workspace_bytes=-1), 1, b"workspace_bytes must be non-negative"),
+    (dict(dtype=2), 1, b"dtype must be 0 (binary16) or 1 (bfloat16)"),
+    (dict(dtype=-1), 1, b"dtype must be"),
 ])
 def test_validation_errors(lib, kw, status, msg):
     p = make(lib, **kw)
@@ -129,6 +131,9 @@ def test_naive_validation(lib):
     p3 = make(lib, seq_len_kv=65)
     assert lib.fa_sm75_naive_forward(ctypes.byref(p3), ctypes.c_void_p(0x10000)) == 1
     assert b"seq_len_kv == seq_len" in lib.fa_sm75_last_error()
+    p4 = make(lib, dtype=1)
+    assert lib.fa_sm75_naive_forward(ctypes.byref(p4), ctypes.c_void_p(0x10000)) == 1
+    assert b"binary16 only" in lib.fa_sm75_last_error()
 
 
 def test_workspace_size(lib):
@@ -203,7 +208,7 @@ def test_mask_param_validation(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_sm75_abi_version() == 2
+    assert lib.fa_sm75_abi_version() == 3
 
 
 def test_kernel_policy_switch(lib):
