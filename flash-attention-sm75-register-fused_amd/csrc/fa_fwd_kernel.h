@@ -1,10 +1,12 @@
 // Fused attention forward kernel for gfx950 (MI355X / CDNA4), included by the
-// instance files fa_fwd_d*.hip (one head dimension and workgroup shape each,
-// compiled in parallel); fa_fwd.hip dispatches between them.
+// instance files fa_fwd_d*.hip (one head dimension, workgroup shape and
+// element type each, compiled in parallel); fa_fwd.hip dispatches between
+// them.
 //
 // O = softmax(scale * Q K^T + mask) V with fp16 inputs, fp32 accumulation and
 // an fp16 output, in one kernel (the hot path that reference
-// src/kernels/flash_attention_forward.cu:345-791 implements for SM75).
+// src/kernels/flash_attention_forward.cu:345-791 implements for SM75); the
+// BF16 instances take bfloat16 Q/K/V/O (bf16 MFMAs, P rounded to bf16).
 //
 // Work decomposition
 //   A 1-D grid of batch * heads_q * ceil(N / kBlockM) workgroups, kBlockM =
