@@ -37,11 +37,17 @@ template <bool BF16>
 void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int policy,
                   hipStream_t stream) {
   const Schedule schedule = schedule_of_policy(policy);
-  if (a.mbits != nullptr)
+  if (a.mbits != nullptr) {
     launch_shape<4, true, false, BF16>(a, batch, head_dim, causal, schedule, stream);
-  else if (policy == 2 && !BF16)
-    launch_shape<8, false, false, false>(a, batch, head_dim, causal, Schedule::kStatic, stream);
-  else if (use_key_split(a, batch, head_dim, causal, policy))
+    return;
+  }
+  if constexpr (!BF16) {
+    if (policy == 2) {
+      launch_shape<8, false, false, false>(a, batch, head_dim, causal, Schedule::kStatic, stream);
+      return;
+    }
+  }
+  if (use_key_split(a, batch, head_dim, causal, policy))
     launch_shape<8, false, true, BF16>(a, batch, head_dim, causal, Schedule::kStatic, stream);
   else
     launch_shape<4, false, false, BF16>(a, batch, head_dim, causal, schedule, stream);
