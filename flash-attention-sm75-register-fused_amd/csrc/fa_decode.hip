@@ -248,14 +248,13 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
       m_run = m_new;
     }
     const float mc = ((m_run == -__builtin_inff()) ? 0.0f : m_run) * c2;
-    half8 pf[2];
+    uint4v pf[2];  // P operands as 32-bit lanes (pairs written whole)
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
       const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c2, -mc));
       const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i + 1], c2, -mc));
       const half2v pr = E::pack(p0, p1);
-      pf[i >> 3][i & 7] = pr[0];
-      pf[i >> 3][(i & 7) + 1] = pr[1];
+      pf[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, pr);
       l_run = E::sum2(pr, l_run);
     }
     // V of this tile has landed once only the next tile's loads are pending
@@ -267,7 +266,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
 #pragma unroll
     for (int v = 0; v < NPV; ++v) {
       const int ks = v / MT, mt = v % MT;
-      oacc[mt] = E::mfma(vf[v], pf[ks], oacc[mt]);
+      oacc[mt] = E::mfma(vf[v], __builtin_bit_cast(half8, pf[ks]), oacc[mt]);
     }
   };
 

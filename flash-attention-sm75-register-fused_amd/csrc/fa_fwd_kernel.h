@@ -444,7 +444,10 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       constexpr int PV_FIRST = ns;                    // slot of the first P V MFMA
       constexpr int PAIR_SLOTS = NB - MT;             // slots available to pairs
       half8 kf[NS];
-      half8 pf[4];
+      // P operands as 32-bit lanes: each converted pair is written whole
+      // (inserting its two halves one by one makes the compiler convert and
+      // repack per element).
+      uint4v pf[4];
       half8 vf[NPV];
       constexpr auto pair_slot = [](int p) constexpr {
         const int spread = (p * PAIR_SLOTS) / 16;
@@ -468,8 +471,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i], c2, -mc));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i + 1], c2, -mc));
         const half2v pr = E::pack(p0, p1);
-        pf[2 * t + (i >> 3)][i & 7] = pr[0];
-        pf[2 * t + (i >> 3)][(i & 7) + 1] = pr[1];
+        pf[2 * t + (i >> 3)][(i & 7) >> 1] = __builtin_bit_cast(unsigned, pr);
         l_run = E::sum2(pr, l_run);
         // Keeps the row-sum update in this slot: left alone, the compiler
         // sinks all 16 of a step's (serially dependent) updates, with
@@ -504,7 +506,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         } else {
           constexpr int v = slot - PV_FIRST;
           constexpr int ks = v / MT, mt = v % MT;
-          oacc[mt] = E::mfma(vf[v], pf[ks], oacc[mt]);
+          oacc[mt] = E::mfma(vf[v], __builtin_bit_cast(half8, pf[ks]), oacc[mt]);
         }
         if constexpr (HAS_NEXT) {
           static_for<LPW>([&](auto q_c) {
