@@ -107,13 +107,15 @@ int64_t tile_steps_per_head(const FwdArgs& a, bool causal) {
 constexpr int64_t kDynamicMinSteps = 1024;
 
 // AUTO takes key-split workgroups at head_dim 128 for causal launches of at
-// most this many 128-row blocks per resident 128-row workgroup: every block
-// gets a slot at once, so the largest block's chain of key tiles sets the
-// launch time, and the split halves it.  Measured on MI355X (interleaved
-// A/B): B=1 Hq=8 N=8192 +14-16%, B=1 Hq=32 N=2048 +1%; with more blocks
-// than slots 5-13% slower; at head_dim 64 2-3% slower (its steps are bound
-// by the softmax arithmetic, not by the chain).
+// most this many 128-row blocks per resident 128-row workgroup, each block
+// row at least kSplitMinBlocks long: every block gets a slot at once, so the
+// largest block's chain of key tiles sets the launch time, and the split
+// halves it.  Measured on MI355X (interleaved A/B against the 4-wave kernel
+// with paired blocks): 16 blocks per row 0.955x, 32 1.02-1.03x, 48-128
+// 1.09x; with more blocks than slots 5-13% slower; at head_dim 64 2-3%
+// slower (its steps are bound by the softmax arithmetic, not the chain).
 constexpr int64_t kSplitMaxItems = 1;
+constexpr int kSplitMinBlocks = 32;
 
 }  // namespace
 
@@ -123,7 +125,8 @@ bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int p
   if (policy != 0 || !causal || head_dim != 128) return false;
   FwdArgs planned = a;
   plan_grid(planned, batch, 128);
-  return planned.items <= kSplitMaxItems * resident_fused_workgroups();
+  return planned.num_qblocks >= kSplitMinBlocks &&
+         planned.items <= kSplitMaxItems * resident_fused_workgroups();
 }
 
 bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedule schedule) {

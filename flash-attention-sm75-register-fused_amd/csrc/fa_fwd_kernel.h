@@ -674,11 +674,16 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
   const bool same = a.ksn == a.vsn;
   FwdArgs args = a;
   int64_t wgs = plan_grid(args, batch, KSPLIT ? 128 : 32 * WAVES);
+  const int64_t slots = resident_fused_workgroups();
   if (WAVES == 4 && args.ctr != nullptr && use_dynamic_schedule(args, batch, causal, schedule)) {
     launch_clear_tickets(args.ctr, stream);
-    wgs = std::min<int64_t>(wgs, resident_fused_workgroups());
+    wgs = std::min<int64_t>(wgs, slots);
   } else {
     args.ctr = nullptr;
+    // Two 4-wave workgroups per CU, all blocks resident at once: pair large
+    // and small causal blocks on each CU (block_work).
+    if (WAVES == 4 && !KSPLIT && causal && wgs <= slots)
+      args.pair_half = (int)(slots / 2 / args.xcds);
   }
   const dim3 grid((unsigned)wgs);
   const dim3 block(64 * WAVES);

@@ -36,6 +36,7 @@ struct FwdArgs {
   uint64_t* ctr;    // queue counters of the dynamic schedule, or nullptr (static)
   int items;        // work items (query blocks): filled by the launcher
   int bf16;         // elements are bfloat16 (else binary16)
+  int pair_half;    // > 0: single-round causal order pairing (launcher; block_work)
 };
 
 // Dynamic schedule of the fused kernel: one 64-bit (head, tail) counter per
@@ -71,6 +72,7 @@ inline int64_t plan_grid(FwdArgs& a, int batch, int block_m) {
   a.units = batch * (a.hq / a.group);
   a.xcds = a.units % kNumXcds == 0 ? kNumXcds : 1;
   a.items = batch * a.hq * a.num_qblocks;
+  a.pair_half = 0;
   return a.items;
 }
 // Whether the 4-wave kernel runs the dynamic schedule for a planned call

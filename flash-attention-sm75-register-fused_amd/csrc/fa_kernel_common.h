@@ -173,12 +173,19 @@ __device__ __forceinline__ void static_for(F&& f) {
 //  * Within a sequence, workgroups go rank-major: rank r of every head before
 //    rank r+1.  Under causal masking rank 0 is the last (most expensive)
 //    query block, so the cheap blocks fill the tail of the launch.
+//  * a.pair_half > 0 (a causal launch that fits the GPU in one round): an
+//    XCD hands its first 2 * CUs workgroups out so that sequence positions p
+//    and p + pair_half share a CU (pair_half = CUs per XCD, times 8 with one
+//    sequence).  Positions from pair_half on then hold the ranks in reverse,
+//    so each CU gets a large and a small block: C3's CUs hold 34 key tiles
+//    each instead of 20..48.
 struct Work {
   int b, hq, hkv, qb;
 };
 __device__ __forceinline__ Work block_work(const FwdArgs& a, int wg, bool causal) {
   const int x = wg % a.xcds;
-  const int p = wg / a.xcds;
+  int p = wg / a.xcds;
+  if (a.pair_half > 0 && p >= a.pair_half) p = a.items / a.xcds - 1 + a.pair_half - p;
   const int per = a.units / a.xcds;   // units of this sequence
   const int row = per * a.group;      // workgroups per rank
   const int rank = p / row;

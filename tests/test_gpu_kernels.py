@@ -70,6 +70,10 @@ SHAPES = [
     (1, 2, 2, 65, 64, True),
     (1, 2, 2, 130, 128, False),      # 3 key tiles: odd split
     (4, 8, 8, 2048, 64, True),       # C3
+    # single-round causal launches, whose blocks are laid out in pairs
+    (1, 36, 3, 1700, 64, True),      # one sequence (3 units), 504 blocks
+    (2, 16, 8, 2000, 128, True),     # 8 sequences, exactly 512 blocks
+    (1, 24, 8, 2048, 64, True),      # 8 sequences, 384 blocks (half the pairs)
 ]
 
 
@@ -102,7 +106,7 @@ def test_key_split_auto_picks_one(device):
     """The automatic choice equals a forced kernel bit for bit: key-split
     workgroups on small causal launches at head_dim 128, 128-row ones
     otherwise; the two kernels differ only by the merge's rounding."""
-    for (B, Hq, Hkv, N, D) in ((1, 8, 8, 2100, 128), (4, 8, 8, 2048, 64), (2, 32, 8, 2048, 128)):
+    for (B, Hq, Hkv, N, D) in ((1, 4, 4, 4200, 128), (4, 8, 8, 2048, 64), (2, 32, 8, 2048, 128)):
         q, k, v = (t.to(device) for t in inputs(B, Hq, Hkv, N, D, seed=B + N + D))
         outs = {}
         for pol in (0, NARROW, SPLIT):
