@@ -240,6 +240,98 @@ std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_
   return {O, L};
 }
 
+// ---- flash_attention_backward: dQ, dK, dV (no reference counterpart) ---------
+
+// Gradients of flash_attention_forward_ex's O (causal code and scale as
+// given to it) from dO, the inputs, O and the fp32 row LSE it returned.
+// Inputs are read in place when their layout allows; the gradients are
+// dense tensors shaped like Q, K and V.
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_backward(
+    torch::Tensor dO, torch::Tensor Q, torch::Tensor K, torch::Tensor V, torch::Tensor O,
+    torch::Tensor LSE, int64_t causal, double scale) {
+  for (auto* pr : {&Q, &K, &V, &O, &dO}) {
+    const torch::Tensor& t = *pr;
+    TORCH_CHECK(t.is_cuda(), "inputs must be CUDA tensors");
+    TORCH_CHECK(t.dtype() == torch::kFloat16 || t.dtype() == torch::kBFloat16,
+                "inputs must be FP16 or BF16");
+    TORCH_CHECK(t.dtype() == Q.dtype(), "Q, K, V, O and dO must have the same dtype");
+    TORCH_CHECK(t.dim() == 4, "inputs must be [B, H, N, D]");
+    TORCH_CHECK(t.device() == Q.device(), "inputs must be on the same device");
+  }
+  TORCH_CHECK(Q.size(0) == K.size(0), "batch mismatch");
+  TORCH_CHECK(K.size(1) > 0 && Q.size(1) % K.size(1) == 0, "heads mismatch: Q heads (",
+              Q.size(1), ") not divisible by K/V heads (", K.size(1), ")");
+  TORCH_CHECK(Q.size(3) == K.size(3), "head_dim mismatch");
+  TORCH_CHECK(K.sizes() == V.sizes(), "K and V must have identical shapes");
+  TORCH_CHECK(O.sizes() == Q.sizes() && dO.sizes() == Q.sizes(), "O and dO must be shaped like Q");
+  TORCH_CHECK(LSE.device() == Q.device() && LSE.dtype() == torch::kFloat32,
+              "LSE must be a float32 tensor on Q's device");
+  TORCH_CHECK(LSE.dim() == 3 && LSE.size(0) == Q.size(0) && LSE.size(1) == Q.size(1) &&
+                  LSE.size(2) == Q.size(2),
+              "LSE must be [B, Hq, N]");
+  TORCH_CHECK(causal >= 0 && causal <= 2,
+              "causal must be 0 (none), 1 (top-left) or 2 (bottom-right), got ", causal);
+  const auto D = Q.size(3);
+  TORCH_CHECK(D == 64 || D == 128, "flash_attention_backward supports head_dim=64 or 128, got ",
+              D);
+  Q = kernel_view(Q, true);  // Q and dO tiles go through buffer windows too
+  dO = kernel_view(dO, true);
+  K = kernel_view(K, true);
+  V = kernel_view(V, true);
+  O = kernel_view(O, false);
+  LSE = LSE.contiguous();
+  auto dQ = torch::empty(Q.sizes(), Q.options());
+  auto dK = torch::empty(K.sizes(), K.options());
+  auto dV = torch::empty(V.sizes(), V.options());
+  if (Q.numel() == 0 && K.numel() == 0) return {dQ, dK, dV};
+  if (Q.size(1) == 0) return {dQ, dK.zero_(), dV.zero_()};  // no query head reads K/V
+  TORCH_CHECK(K.size(2) > 0 || Q.size(2) == 0, "K/V must hold at least one row");
+  const at::OptionalDeviceGuard guard(at::device_of(Q));
+  fa_bwd_params p{};
+  p.q = static_cast<const fa_half*>(Q.data_ptr());
+  p.k = static_cast<const fa_half*>(K.data_ptr());
+  p.v = static_cast<const fa_half*>(V.data_ptr());
+  p.o = static_cast<const fa_half*>(O.data_ptr());
+  p.dout = static_cast<const fa_half*>(dO.data_ptr());
+  p.lse = LSE.data_ptr<float>();
+  p.dq = static_cast<fa_half*>(dQ.data_ptr());
+  p.dk = static_cast<fa_half*>(dK.data_ptr());
+  p.dv = static_cast<fa_half*>(dV.data_ptr());
+  p.batch = Q.size(0);
+  p.heads_q = Q.size(1);
+  p.heads_kv = K.size(1);
+  p.seq_len = Q.size(2);
+  p.seq_len_kv = K.size(2);
+  p.head_dim = D;
+  auto strides = [&](const torch::Tensor& t, int64_t& sb, int64_t& sh, int64_t& sn) {
+    sn = eff_stride(t, 2, D);
+    sh = eff_stride(t, 1, 0);
+    sb = eff_stride(t, 0, 0);
+  };
+  strides(Q, p.q_stride_b, p.q_stride_h, p.q_stride_n);
+  strides(K, p.k_stride_b, p.k_stride_h, p.k_stride_n);
+  strides(V, p.v_stride_b, p.v_stride_h, p.v_stride_n);
+  strides(O, p.o_stride_b, p.o_stride_h, p.o_stride_n);
+  strides(dO, p.do_stride_b, p.do_stride_h, p.do_stride_n);
+  strides(dQ, p.dq_stride_b, p.dq_stride_h, p.dq_stride_n);
+  strides(dK, p.dk_stride_b, p.dk_stride_h, p.dk_stride_n);
+  strides(dV, p.dv_stride_b, p.dv_stride_h, p.dv_stride_n);
+  p.scale = (float)scale;
+  p.causal = (int)causal;
+  p.dtype = Q.scalar_type() == torch::kBFloat16 ? FA_DTYPE_BF16 : FA_DTYPE_FP16;
+  p.stream = c10::hip::getCurrentHIPStream(Q.device().index()).stream();
+  const int64_t ws = fa_sm75_backward_workspace_size(&p);
+  torch::Tensor work;  // released after the launch: stream-ordered reuse
+  if (ws > 0) {
+    work = torch::empty({ws}, Q.options().dtype(torch::kUInt8));
+    p.workspace = work.data_ptr();
+    p.workspace_bytes = ws;
+  }
+  const int st = fa_sm75_backward(&p);
+  TORCH_CHECK(st == FA_OK, "flash_attention_backward: ", fa_sm75_last_error());
+  return {dQ, dK, dV};
+}
+
 torch::Tensor d64_compat(const char* tag, torch::Tensor Q, torch::Tensor K,
                          torch::Tensor V, bool causal, float scale) {
   check_tensor(Q, "Q");
@@ -301,6 +393,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("Q"), pybind11::arg("K"), pybind11::arg("V"), pybind11::arg("causal"),
         pybind11::arg("scale"), pybind11::arg("return_lse") = false,
         pybind11::arg("attn_mask") = pybind11::none());
+  m.def("flash_attention_backward", &flash_attention_backward,
+        "(dQ, dK, dV) of flash_attention_forward_ex's output from dO, Q, K, V, O and the "
+        "fp32 row LSE; causal 0 none, 1 top-left, 2 bottom-right",
+        pybind11::arg("dO"), pybind11::arg("Q"), pybind11::arg("K"), pybind11::arg("V"),
+        pybind11::arg("O"), pybind11::arg("LSE"), pybind11::arg("causal"),
+        pybind11::arg("scale"));
   m.def("abi_version", []() { return fa_sm75_abi_version(); });
   m.def("set_kernel_policy", [](int policy) {
     TORCH_CHECK(fa_sm75_set_kernel_policy(policy) == FA_OK,

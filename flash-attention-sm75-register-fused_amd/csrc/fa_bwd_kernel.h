@@ -1,0 +1,487 @@
+// Fused attention backward kernels for gfx950 (MI355X / CDNA4), included by
+// the instance files fa_bwd_d64.hip and fa_bwd_d128.hip.
+//
+// Gradients of O = softmax(scale * Q K^T + mask) V, given dO = dL/dO, the
+// forward's O and its row log-sum-exp (no reference counterpart: the
+// reference's autograd backward raises, src/flash_attention_sm75/ops.py:47-52):
+//   P = exp(scale * Q K^T - LSE)            (recomputed, never stored)
+//   dV = P^T dO,  dP = dO V^T,  dS = P o (dP - rowsum(dO o O)),
+//   dQ = scale * dS K,  dK = scale * dS^T Q.
+// P and dS are rounded to the element type before the products that take
+// them, as the forward rounds P; everything else accumulates in fp32.
+//
+// Three kernels, all deterministic (no atomics: every gradient element is
+// summed by one wave in a fixed order):
+//   * fa_bwd_stats_kernel: per query row lse * log2(e) and rowsum(dO o O),
+//     into the workspace in 64-row records (one direct load per tile).
+//   * fa_bwd_dkdv_kernel: one workgroup per (batch, KV head, 128 keys), wave
+//     w owning keys k0 + 32w .. +32 with their K and V rows resident in
+//     registers.  It streams 64-row tiles of Q and dO (and their stats)
+//     through LDS for every query head of the group, so the GQA sum over
+//     the group happens in the accumulators.
+//   * fa_bwd_dq_kernel: one workgroup per (batch, query head, 128 rows), the
+//     forward's shape: Q and dO rows resident, K and V tiles streamed.
+// Tiles use the forward's LDS layout (Lds<D>: padded rows, 16-byte chunks
+// XOR-swizzled), on which both operand reads below are conflict-free.
+//
+// MFMA layouts (v_mfma_f32_32x32x16, as in fa_fwd_kernel.h):
+//   A[m][k]: lane l holds m = l%32, k = 8*(l/32) + j
+//   B[k][n]: lane l holds n = l%32, k = 8*(l/32) + j
+//   C[m][n]: lane l holds n = l%32, m = 8*(i/4) + 4*(l/32) + i%4
+// dK/dV kernel: S = Q K^T and dP = dO V^T with queries on M and keys on N,
+// so each lane owns one key; dV^T += dO^T P and dK^T += Q^T dS take P and dS
+// straight from those accumulators as B operands (16-query steps in the row
+// order C hands over), with dO^T and Q^T read transposed out of the tiles.
+// dQ kernel: S^T = K Q^T and dP^T = V dO^T (lane = query, so LSE and the
+// row sum are per-lane scalars), dQ^T += K^T dS^T.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fa_internal.h"
+
+#include "fa_kernel_common.h"
+
+namespace fa {
+namespace {
+
+// Per-lane LDS addressing in one Lds<D> tile (64 rows):
+//   row(t, kk): the 8 columns 16kk + 8(l/32) .. +8 of row 32t + l%32 (an A
+//               or B operand whose m or n index is the tile row);
+//   tr(ks, mt): the A operand X^T of the row-major tile X: column 32mt + l%32
+//               of rows 16ks + {4(l/32) + 0..3, 8 + 4(l/32) + 0..3}, the
+//               order in which an accumulator's 16 rows arrive as B (two
+//               transposing ds_read_b64_tr_b16, 16 lanes = 4 rows x 16 columns).
+template <int D>
+struct TileReader {
+  using L = Lds<D>;
+  int row_even, row_odd, tr0, tr1;
+  __device__ __forceinline__ explicit TileReader(int lane) {
+    const int hi = lane >> 5, ql = lane & 31, grp = lane >> 4, gi = lane & 15;
+    const int s = (ql >> 2) & 3;
+    row_even = ql * L::Pitch + 8 * (hi ^ s);
+    row_odd = ql * L::Pitch + 8 * ((2 + hi) ^ s);
+    const int r = 4 * hi + (gi >> 2);
+    const int c = 2 * (grp & 1) + ((gi & 3) >> 1);
+    tr0 = r * L::Pitch + 8 * (c ^ hi) + 4 * (gi & 1);
+    tr1 = (r + 8) * L::Pitch + 8 * (c ^ (hi + 2)) + 4 * (gi & 1);
+  }
+  __device__ __forceinline__ half8 row(const _Float16* tile, int t, int kk) const {
+    const int off = ((kk & 1) ? row_odd : row_even) + 32 * t * L::Pitch + 32 * (kk >> 1);
+    return *(const half8*)(tile + off);
+  }
+  __device__ __forceinline__ half8 tr(const _Float16* tile, int ks, int mt) const {
+    const int imm = 16 * ks * L::Pitch + 32 * mt;
+    const half4 lo = ds_read_tr16(tile + tr0 + imm);
+    const half4 hi4 = ds_read_tr16(tile + tr1 + imm);
+    return __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+};
+
+// Global byte offset of lane `lane`'s 16 bytes in 1 KB segment `seg` of an
+// Lds<D> tile whose source rows are `stride` elements apart; -16 (past any
+// buffer window, so the lane writes zeros) for bytes in the row padding.
+template <int D>
+__device__ __forceinline__ int seg_offset(int seg, int lane, int64_t stride) {
+  using L = Lds<D>;
+  const int pos = seg * 1024 + 16 * lane;
+  const int row = pos / (2 * L::Pitch);
+  const int within = pos - row * (2 * L::Pitch);
+  if (within >= 2 * D) return -16;
+  const int c = (within >> 4) ^ ((row >> 2) & 3);
+  return (int)(row * stride * 2) + 16 * c;
+}
+
+// P or dS values of accumulator elements i, i+1 of 32-row sub-tile t as one
+// packed 32-bit lane of the B operand of 16-row step 2t + (i >> 3).
+template <class E, int NOPS>
+__device__ __forceinline__ void put_pair(uint4v (&ops)[NOPS], int t, int i, float x, float y) {
+  ops[2 * t + (i >> 3)][(i & 7) >> 1] = __builtin_bit_cast(unsigned, E::pack(x, y));
+}
+
+// ---- stats: lse * log2(e) and rowsum(dO o O) per query row -----------------
+// One workgroup per (b, query head, 64-row tile); wave w takes rows 16w..16w+15,
+// D/8 lanes per row (16 bytes each).
+template <int D, bool BF16>
+__global__ void __launch_bounds__(256) fa_bwd_stats_kernel(const BwdArgs a) {
+  using E = Elem<BF16>;
+  constexpr int LPR = D / 8;      // lanes per row
+  constexpr int RPP = 64 / LPR;   // rows per pass
+  const int rec = (int)blockIdx.x;  // (b * hq + h) * qtiles + qt
+  const int bh = rec / a.qtiles;
+  const int qt = rec - bh * a.qtiles;
+  const int b = bh / a.hq, hq = bh - b * a.hq;
+  const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+  const int sub = lane / LPR, part = lane - sub * LPR;
+  float* const out = a.stats + (int64_t)rec * (2 * kBwdStatsTile);
+#pragma unroll
+  for (int r0 = 16 * wave; r0 < 16 * wave + 16; r0 += RPP) {
+    const int r = r0 + sub;
+    const int row = qt * kBwdStatsTile + r;
+    float acc = 0.0f;
+    if (row < a.n) {
+      const half8 o8 =
+          *(const half8*)(a.o + b * a.osb + hq * a.osh + (int64_t)row * a.osn + 8 * part);
+      const half8 d8 =
+          *(const half8*)(a.dout + b * a.dosb + hq * a.dosh + (int64_t)row * a.dosn + 8 * part);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(E::to_f32(o8[j]), E::to_f32(d8[j]), acc);
+    }
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (part == 0) {
+      float l2 = __builtin_inff();
+      if (row < a.n) {
+        const float l = a.lse[(int64_t)bh * a.n + row];
+        l2 = (l == -__builtin_inff()) ? __builtin_inff() : l * 1.4426950408889634f;
+      }
+      out[r] = l2;
+      out[kBwdStatsTile + r] = row < a.n ? acc : 0.0f;
+    }
+  }
+}
+
+// ---- dK, dV ------------------------------------------------------------------
+// Step s of a workgroup: query head hkv * group + s / per_head, query tile
+// qt_begin + s % per_head (causal: the first tile with a query that sees one
+// of the block's keys).  Tiles are double buffered: step s loads step s+1's
+// Q, dO and stats while it computes, then one barrier.
+template <int D, bool CAUSAL, bool BF16>
+__global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
+  using L = Lds<D>;
+  using E = Elem<BF16>;
+  constexpr int KK = D / 16;
+  constexpr int MT = D / 32;
+  constexpr int SEGQ = L::Segs / 4;
+  __shared__ __attribute__((aligned(1024))) _Float16 q_lds0[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 q_lds1[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 d_lds0[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 d_lds1[L::Tile];
+  // 128 floats of stats per tile; a whole-wave direct load writes 1 KB.
+  __shared__ __attribute__((aligned(1024))) float s_lds0[256];
+  __shared__ __attribute__((aligned(1024))) float s_lds1[256];
+
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = (int)threadIdx.x & 63;
+  const int hi = lane >> 5, ql = lane & 31;
+
+  // Work item: XCD x takes the units (b, hkv) [x U/8, (x+1) U/8) when
+  // a.xcds == 8, key blocks in rank order (causal: block 0, which sees the
+  // most queries, first).
+  const int wg = (int)blockIdx.x;
+  const int x = wg % a.xcds, p = wg / a.xcds;
+  const int per = a.units / a.xcds;
+  const int kb = p / per;
+  const int u = x * per + (p - kb * per);
+  const int hkv_count = a.hq / a.group;
+  const int b = u / hkv_count, hkv = u - b * hkv_count;
+  const int k0 = kb * kBwdBlockKeys;
+  const int kw = k0 + 32 * wave;  // this wave's first key
+  const int krow = kw + ql;       // this lane's key
+  const int N = a.n, NK = a.nk;
+
+  // K and V rows of the lane's key as B operands (n = key, k = dims).
+  half8 kf[KK], vf[KK];
+  if (krow < NK) {
+    const _Float16* kp = a.k + b * a.ksb + hkv * a.ksh + (int64_t)krow * a.ksn + 8 * hi;
+    const _Float16* vp = a.v + b * a.vsb + hkv * a.vsh + (int64_t)krow * a.vsn + 8 * hi;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      kf[kk] = *(const half8*)(kp + 16 * kk);
+      vf[kk] = *(const half8*)(vp + 16 * kk);
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) kf[kk] = vf[kk] = (half8)(_Float16)0;
+  }
+  float16v dk[MT], dv[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) dk[mt] = dv[mt] = (float16v)0.0f;
+
+  const int qt_begin = CAUSAL ? min(a.qtiles, max(0, k0 - a.diag) / kBwdStatsTile) : 0;
+  const int per_head = a.qtiles - qt_begin;
+  const int steps = a.group * per_head;
+
+  int goff_q[SEGQ], goff_d[SEGQ];
+#pragma unroll
+  for (int s = 0; s < SEGQ; ++s) {
+    goff_q[s] = seg_offset<D>(wave + 4 * s, lane, a.qsn);
+    goff_d[s] = seg_offset<D>(wave + 4 * s, lane, a.dosn);
+  }
+  // Direct loads of step s's Q and dO tiles (wave w: segments w, w+4, ..)
+  // and, by wave 0, its stats record.
+  auto issue = [&](int s, _Float16* qdst, _Float16* ddst, float* sdst) {
+    const int h = s / per_head;
+    const int qt = qt_begin + (s - h * per_head);
+    const int hq = hkv * a.group + h;
+    const int q0 = qt * kBwdStatsTile;
+    const int rows = N - q0;
+    const __amdgpu_buffer_rsrc_t rq =
+        make_rsrc(a.q + b * a.qsb + hq * a.qsh + (int64_t)q0 * a.qsn, (int)(rows * a.qsn * 2));
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(
+        a.dout + b * a.dosb + hq * a.dosh + (int64_t)q0 * a.dosn, (int)(rows * a.dosn * 2));
+#pragma unroll
+    for (int s2 = 0; s2 < SEGQ; ++s2) {
+      direct_load16(rq, (lds_void*)(qdst + (wave + 4 * s2) * 512), goff_q[s2]);
+      direct_load16(rd, (lds_void*)(ddst + (wave + 4 * s2) * 512), goff_d[s2]);
+    }
+    if (wave == 0) {
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc(
+          a.stats + ((int64_t)(b * a.hq + hq) * a.qtiles + qt) * (2 * kBwdStatsTile),
+          2 * kBwdStatsTile * 4);
+      direct_load16(rs, (lds_void*)sdst, 16 * lane);
+    }
+  };
+
+  const TileReader<D> rd(lane);
+  const float c2 = a.c2;
+
+  auto step = [&](int s, auto par_t) {
+    constexpr int PAR = decltype(par_t)::value;
+    const _Float16* qc = PAR ? q_lds1 : q_lds0;
+    const _Float16* dc = PAR ? d_lds1 : d_lds0;
+    const float* sc = PAR ? s_lds1 : s_lds0;
+    if (s + 1 < steps) issue(s + 1, PAR ? q_lds0 : q_lds1, PAR ? d_lds0 : d_lds1,
+                             PAR ? s_lds0 : s_lds1);
+    const int h = s / per_head;
+    const int qbase = (qt_begin + (s - h * per_head)) * kBwdStatsTile;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float16v sa = (float16v)0.0f, dpa = (float16v)0.0f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) sa = E::mfma(rd.row(qc, t, kk), kf[kk], sa);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) dpa = E::mfma(rd.row(dc, t, kk), vf[kk], dpa);
+      // Element i: query qbase + 32t + 8(i/4) + 4hi + i%4, key krow.
+      const bool need_mask = CAUSAL && kw + 31 > qbase + 32 * t + a.diag;
+      uint4v pp[2], pd[2];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 l4 = *(const float4*)(sc + 32 * t + 8 * g + 4 * hi);
+        const float4 d4 = *(const float4*)(sc + kBwdStatsTile + 32 * t + 8 * g + 4 * hi);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float dl[4] = {d4.x, d4.y, d4.z, d4.w};
+        float pv[4], dsv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * g + e;
+          float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i], c2, -lv[e]));
+          if (need_mask && krow > qbase + 32 * t + 8 * g + 4 * hi + e + a.diag) pe = 0.0f;
+          pv[e] = pe;
+          dsv[e] = pe * (dpa[i] - dl[e]);
+        }
+        put_pair<E>(pp, 0, 4 * g, pv[0], pv[1]);
+        put_pair<E>(pp, 0, 4 * g + 2, pv[2], pv[3]);
+        put_pair<E>(pd, 0, 4 * g, dsv[0], dsv[1]);
+        put_pair<E>(pd, 0, 4 * g + 2, dsv[2], dsv[3]);
+      }
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          dv[mt] = E::mfma(rd.tr(dc, 2 * t + h2, mt), __builtin_bit_cast(half8, pp[h2]), dv[mt]);
+          dk[mt] = E::mfma(rd.tr(qc, 2 * t + h2, mt), __builtin_bit_cast(half8, pd[h2]), dk[mt]);
+        }
+      }
+    }
+    // This wave's loads for step s+1 have landed, and every wave is done
+    // reading the buffers that step s+1 refills for step s+2.
+    barrier_after_loads<0>();
+  };
+
+  if (steps > 0) issue(0, q_lds0, d_lds0, s_lds0);
+  barrier_after_loads<0>();
+  int s = 0;
+  for (; s + 1 < steps; s += 2) {
+    step(s, std::integral_constant<int, 0>{});
+    step(s + 1, std::integral_constant<int, 1>{});
+  }
+  if (s < steps) step(s, std::integral_constant<int, 0>{});
+
+  if (krow < NK) {
+    _Float16* dkp = a.dk + b * a.dksb + hkv * a.dksh + (int64_t)krow * a.dksn;
+    _Float16* dvp = a.dv + b * a.dvsb + hkv * a.dvsh + (int64_t)krow * a.dvsn;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        half4 vk, vv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vk[e] = E::round(dk[mt][4 * g + e] * a.scale);
+          vv[e] = E::round(dv[mt][4 * g + e]);
+        }
+        *(half4*)(dkp + 32 * mt + 8 * g + 4 * hi) = vk;
+        *(half4*)(dvp + 32 * mt + 8 * g + 4 * hi) = vv;
+      }
+    }
+  }
+}
+
+// ---- dQ ----------------------------------------------------------------------
+// The forward's work decomposition (block_work; causal: largest block
+// first): wave w owns query rows q0 + 32w .. +32 and walks the 64-key tiles
+// its block can see, K and V tiles double buffered through LDS.
+template <int D, bool CAUSAL, bool BF16>
+__global__ void __launch_bounds__(256, 1) fa_bwd_dq_kernel(const BwdArgs a) {
+  using L = Lds<D>;
+  using E = Elem<BF16>;
+  constexpr int KK = D / 16;
+  constexpr int MT = D / 32;
+  constexpr int SEGQ = L::Segs / 4;
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds0[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 k_lds1[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds0[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 v_lds1[L::Tile];
+
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = (int)threadIdx.x & 63;
+  const int hi = lane >> 5, ql = lane & 31;
+  const Work w = block_work(a, (int)blockIdx.x, CAUSAL);
+  const int b = w.b, hq = w.hq, hkv = w.hkv;
+  const int bh = b * a.hq + hq;
+  const int q0 = w.qb * kBwdBlockRows;
+  const int qw = q0 + 32 * wave;
+  const int qrow = qw + ql;
+  const int N = a.n, NK = a.nk;
+
+  // Q and dO rows of the lane's query as B operands (n = query, k = dims).
+  half8 qf[KK], df[KK];
+  float lse2 = __builtin_inff(), delta = 0.0f;
+  if (qrow < N) {
+    const _Float16* qp = a.q + b * a.qsb + hq * a.qsh + (int64_t)qrow * a.qsn + 8 * hi;
+    const _Float16* dp = a.dout + b * a.dosb + hq * a.dosh + (int64_t)qrow * a.dosn + 8 * hi;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      qf[kk] = *(const half8*)(qp + 16 * kk);
+      df[kk] = *(const half8*)(dp + 16 * kk);
+    }
+    const float* st = a.stats + ((int64_t)bh * a.qtiles + qrow / kBwdStatsTile) * (2 * kBwdStatsTile);
+    lse2 = st[qrow % kBwdStatsTile];
+    delta = st[kBwdStatsTile + qrow % kBwdStatsTile];
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qf[kk] = df[kk] = (half8)(_Float16)0;
+  }
+  float16v dq[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) dq[mt] = (float16v)0.0f;
+
+  const int kv_len = CAUSAL ? max(0, min(NK, q0 + kBwdBlockRows + a.diag)) : NK;
+  const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
+
+  int goff_k[SEGQ], goff_v[SEGQ];
+#pragma unroll
+  for (int s = 0; s < SEGQ; ++s) {
+    goff_k[s] = seg_offset<D>(wave + 4 * s, lane, a.ksn);
+    goff_v[s] = seg_offset<D>(wave + 4 * s, lane, a.vsn);
+  }
+  const _Float16* Kp = a.k + b * a.ksb + hkv * a.ksh;
+  const _Float16* Vp = a.v + b * a.vsb + hkv * a.vsh;
+  auto issue = [&](int j, _Float16* kdst, _Float16* vdst) {
+    const int rows = NK - j * kBlockN;
+    const __amdgpu_buffer_rsrc_t rk =
+        make_rsrc(Kp + (int64_t)j * kBlockN * a.ksn, (int)(rows * a.ksn * 2));
+    const __amdgpu_buffer_rsrc_t rv =
+        make_rsrc(Vp + (int64_t)j * kBlockN * a.vsn, (int)(rows * a.vsn * 2));
+#pragma unroll
+    for (int s2 = 0; s2 < SEGQ; ++s2) {
+      direct_load16(rk, (lds_void*)(kdst + (wave + 4 * s2) * 512), goff_k[s2]);
+      direct_load16(rv, (lds_void*)(vdst + (wave + 4 * s2) * 512), goff_v[s2]);
+    }
+  };
+
+  const TileReader<D> rd(lane);
+  const float c2 = a.c2;
+
+  auto step = [&](int j, auto par_t) {
+    constexpr int PAR = decltype(par_t)::value;
+    const _Float16* kc = PAR ? k_lds1 : k_lds0;
+    const _Float16* vc = PAR ? v_lds1 : v_lds0;
+    if (j + 1 < ntiles) issue(j + 1, PAR ? k_lds0 : k_lds1, PAR ? v_lds0 : v_lds1);
+    const int kstart = j * kBlockN;
+    const bool need_mask = kstart + kBlockN > NK || (CAUSAL && kstart + kBlockN - 1 > qw + a.diag);
+    uint4v pd[4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float16v sa = (float16v)0.0f, dpa = (float16v)0.0f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) sa = E::mfma(rd.row(kc, t, kk), qf[kk], sa);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) dpa = E::mfma(rd.row(vc, t, kk), df[kk], dpa);
+      // Element i: key kstart + 32t + 8(i/4) + 4hi + i%4, query qrow.
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i], c2, -lse2));
+        float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i + 1], c2, -lse2));
+        if (need_mask) {
+          const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
+          if (key >= NK || (CAUSAL && key > qrow + a.diag)) p0 = 0.0f;
+          if (key + 1 >= NK || (CAUSAL && key + 1 > qrow + a.diag)) p1 = 0.0f;
+        }
+        put_pair<E>(pd, t, i, p0 * (dpa[i] - delta), p1 * (dpa[i + 1] - delta));
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        dq[mt] = E::mfma(rd.tr(kc, ks, mt), __builtin_bit_cast(half8, pd[ks]), dq[mt]);
+    }
+    barrier_after_loads<0>();
+  };
+
+  if (ntiles > 0) issue(0, k_lds0, v_lds0);
+  barrier_after_loads<0>();
+  int j = 0;
+  for (; j + 1 < ntiles; j += 2) {
+    step(j, std::integral_constant<int, 0>{});
+    step(j + 1, std::integral_constant<int, 1>{});
+  }
+  if (j < ntiles) step(j, std::integral_constant<int, 0>{});
+
+  if (qrow < N) {
+    _Float16* op = a.dq + b * a.dqsb + hq * a.dqsh + (int64_t)qrow * a.dqsn;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        half4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = E::round(dq[mt][4 * g + e] * a.scale);
+        *(half4*)(op + 32 * mt + 8 * g + 4 * hi) = v;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// Launches the three backward kernels for head dimension D (the launcher in
+// fa_bwd.hip has planned the grids).
+template <int D, bool BF16>
+void launch_bwd(const BwdArgs& a, int batch, bool causal, hipStream_t stream) {
+  const int stats_wgs = batch * a.hq * a.qtiles;
+  const int dkdv_wgs = a.units * ((a.nk + kBwdBlockKeys - 1) / kBwdBlockKeys);
+  const int dq_wgs = a.items;
+  if (stats_wgs > 0)
+    hipLaunchKernelGGL((fa_bwd_stats_kernel<D, BF16>), dim3(stats_wgs), dim3(256), 0, stream, a);
+  if (causal) {
+    if (dkdv_wgs > 0)
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, true, BF16>), dim3(dkdv_wgs), dim3(256), 0,
+                         stream, a);
+    if (dq_wgs > 0)
+      hipLaunchKernelGGL((fa_bwd_dq_kernel<D, true, BF16>), dim3(dq_wgs), dim3(256), 0, stream,
+                         a);
+  } else {
+    if (dkdv_wgs > 0)
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, false, BF16>), dim3(dkdv_wgs), dim3(256), 0,
+                         stream, a);
+    if (dq_wgs > 0)
+      hipLaunchKernelGGL((fa_bwd_dq_kernel<D, false, BF16>), dim3(dq_wgs), dim3(256), 0, stream,
+                         a);
+  }
+}
+
+}  // namespace fa

@@ -201,6 +201,94 @@ void legacy_launch(const char* tag, const fa_half* Q, const fa_half* K, const fa
   if (e != hipSuccess) std::fprintf(stderr, "[%s] %s\n", tag, hipGetErrorString(e));
 }
 
+int64_t bwd_kv_rows(const fa_bwd_params* p) {
+  return p->seq_len_kv != 0 ? p->seq_len_kv : p->seq_len;
+}
+
+bool bwd_empty(const fa_bwd_params* p) {
+  return p->batch == 0 || p->heads_q == 0 || (p->seq_len == 0 && bwd_kv_rows(p) == 0);
+}
+
+// Validation of fa_sm75_backward (the forward's rules for the shared
+// fields, plus the gradient tensors, the LSE and the workspace).
+int validate_bwd(const fa_bwd_params* p) {
+  if (p == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "params must not be NULL");
+  if (p->batch < 0 || p->heads_q < 0 || p->heads_kv < 0 || p->seq_len < 0 ||
+      p->head_dim < 0 || p->seq_len_kv < 0)
+    return fail(FA_ERR_INVALID_ARGUMENT,
+                "sizes must be non-negative (batch=%lld heads_q=%lld heads_kv=%lld "
+                "seq_len=%lld head_dim=%lld)",
+                (long long)p->batch, (long long)p->heads_q, (long long)p->heads_kv,
+                (long long)p->seq_len, (long long)p->head_dim);
+  if (p->head_dim != 64 && p->head_dim != 128)
+    return fail(FA_ERR_UNSUPPORTED_HEAD_DIM,
+                "flash_attention_backward supports head_dim=64 or 128, got %lld",
+                (long long)p->head_dim);
+  if (p->heads_q > 0 && p->heads_kv == 0)
+    return fail(FA_ERR_HEADS_NOT_DIVISIBLE, "heads_kv must be positive");
+  if (p->heads_kv > 0 && (p->heads_q % p->heads_kv) != 0)
+    return fail(FA_ERR_HEADS_NOT_DIVISIBLE,
+                "heads mismatch: Q heads (%lld) not divisible by K/V heads (%lld)",
+                (long long)p->heads_q, (long long)p->heads_kv);
+  if (!std::isfinite(p->scale)) return fail(FA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  if (p->causal < FA_CAUSAL_NONE || p->causal > FA_CAUSAL_BOTTOM_RIGHT)
+    return fail(FA_ERR_INVALID_ARGUMENT,
+                "causal must be 0, 1 (top-left) or 2 (bottom-right), got %d", p->causal);
+  if (p->dtype != FA_DTYPE_FP16 && p->dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_INVALID_ARGUMENT, "dtype must be 0 (binary16) or 1 (bfloat16), got %d",
+                p->dtype);
+  if (bwd_empty(p)) return FA_OK;
+  // With no query rows only dK and dV (zeros) are written, from K and V's shapes.
+  const bool rows = p->seq_len > 0;
+  const void* ptrs[9] = {p->k, p->v, p->dk, p->dv, p->q, p->o, p->dout, p->dq, p->workspace};
+  for (int i = 0; i < (rows ? 9 : 4); ++i)
+    if (ptrs[i] == nullptr)
+      return fail(FA_ERR_INVALID_ARGUMENT,
+                  "Q, K, V, O, dO, dQ, dK, dV and workspace pointers must not be NULL");
+  for (int i = 0; i < (rows ? 9 : 4); ++i)
+    if (!aligned16(ptrs[i]))
+      return fail(FA_ERR_MISALIGNED, "tensor and workspace pointers must be 16-byte aligned");
+  if (rows && p->lse == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "lse must not be NULL");
+  if ((reinterpret_cast<uintptr_t>(p->lse) & 3u) != 0)
+    return fail(FA_ERR_MISALIGNED, "lse must be 4-byte aligned");
+  const int64_t strides[24] = {
+      p->q_stride_b,  p->q_stride_h,  p->q_stride_n,  p->k_stride_b,  p->k_stride_h,
+      p->k_stride_n,  p->v_stride_b,  p->v_stride_h,  p->v_stride_n,  p->o_stride_b,
+      p->o_stride_h,  p->o_stride_n,  p->do_stride_b, p->do_stride_h, p->do_stride_n,
+      p->dq_stride_b, p->dq_stride_h, p->dq_stride_n, p->dk_stride_b, p->dk_stride_h,
+      p->dk_stride_n, p->dv_stride_b, p->dv_stride_h, p->dv_stride_n};
+  for (int i = 0; i < 24; ++i) {
+    if (strides[i] < 0) return fail(FA_ERR_INVALID_ARGUMENT, "strides must be non-negative");
+    if (strides[i] % 8 != 0)
+      return fail(FA_ERR_MISALIGNED,
+                  "batch/head/row strides must be multiples of 8 elements (16 bytes)");
+  }
+  for (int i = 2; i < 24; i += 3)
+    if (strides[i] < p->head_dim)
+      return fail(FA_ERR_INVALID_ARGUMENT, "row stride must be at least head_dim");
+  const int64_t nk = bwd_kv_rows(p);
+  if (p->seq_len > INT32_MAX / 2 || nk > INT32_MAX / 2)
+    return fail(FA_ERR_TOO_LARGE, "seq_len %lld / seq_len_kv %lld exceeds the supported maximum",
+                (long long)p->seq_len, (long long)nk);
+  if (nk == 0 && p->seq_len > 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "K/V must hold at least one row");
+  // Q and dO tiles (dK/dV kernel) and K and V tiles (dQ kernel) are read
+  // through 32-bit buffer windows over one (batch, head).
+  if ((p->seq_len + 64) * p->q_stride_n * 2 > (int64_t)INT32_MAX ||
+      (p->seq_len + 64) * p->do_stride_n * 2 > (int64_t)INT32_MAX ||
+      (nk + 64) * p->k_stride_n * 2 > (int64_t)INT32_MAX ||
+      (nk + 64) * p->v_stride_n * 2 > (int64_t)INT32_MAX)
+    return fail(FA_ERR_TOO_LARGE, "rows * row stride of Q, dO, K or V exceeds 2^31 bytes");
+  if (p->batch * p->heads_q * ((p->seq_len + 63) / 64) >= (int64_t)(1u << 24) ||
+      p->batch * p->heads_kv * ((nk + 127) / 128) >= (int64_t)(1u << 24))
+    return fail(FA_ERR_TOO_LARGE, "the backward grids exceed 2^24 workgroups");
+  const int64_t need = fa::bwd_workspace_bytes(p->batch, p->heads_q, p->seq_len);
+  if (p->workspace_bytes < need)
+    return fail(FA_ERR_INVALID_ARGUMENT, "workspace_bytes %lld is below the required %lld",
+                (long long)p->workspace_bytes, (long long)need);
+  return FA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -293,6 +381,61 @@ int fa_sm75_naive_forward(const fa_fwd_params* p, float* workspace) {
   fa::launch_naive_forward(a, (int)p->batch, (int)p->head_dim, p->causal != 0, p->scale,
                            workspace, reinterpret_cast<hipStream_t>(p->stream));
   return check_launch();
+}
+
+void fa_sm75_set_contiguous_bwd_strides(fa_bwd_params* p) {
+  const int64_t D = p->head_dim, N = p->seq_len, Nk = bwd_kv_rows(p);
+  const int64_t qh = N * D, qb = p->heads_q * N * D, kh = Nk * D, kb = p->heads_kv * Nk * D;
+  p->q_stride_n = D; p->q_stride_h = qh; p->q_stride_b = qb;
+  p->o_stride_n = D; p->o_stride_h = qh; p->o_stride_b = qb;
+  p->do_stride_n = D; p->do_stride_h = qh; p->do_stride_b = qb;
+  p->dq_stride_n = D; p->dq_stride_h = qh; p->dq_stride_b = qb;
+  p->k_stride_n = D; p->k_stride_h = kh; p->k_stride_b = kb;
+  p->v_stride_n = D; p->v_stride_h = kh; p->v_stride_b = kb;
+  p->dk_stride_n = D; p->dk_stride_h = kh; p->dk_stride_b = kb;
+  p->dv_stride_n = D; p->dv_stride_h = kh; p->dv_stride_b = kb;
+}
+
+int fa_sm75_backward(const fa_bwd_params* p) {
+  g_last_error[0] = '\0';
+  const int st = validate_bwd(p);
+  if (st != FA_OK) return st;
+  if (bwd_empty(p)) return FA_OK;
+  fa::BwdArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.q = reinterpret_cast<const _Float16*>(p->q);
+  a.k = reinterpret_cast<const _Float16*>(p->k);
+  a.v = reinterpret_cast<const _Float16*>(p->v);
+  a.o = reinterpret_cast<const _Float16*>(p->o);
+  a.dout = reinterpret_cast<const _Float16*>(p->dout);
+  a.lse = p->lse;
+  a.dq = reinterpret_cast<_Float16*>(p->dq);
+  a.dk = reinterpret_cast<_Float16*>(p->dk);
+  a.dv = reinterpret_cast<_Float16*>(p->dv);
+  a.qsb = p->q_stride_b; a.qsh = p->q_stride_h; a.qsn = p->q_stride_n;
+  a.ksb = p->k_stride_b; a.ksh = p->k_stride_h; a.ksn = p->k_stride_n;
+  a.vsb = p->v_stride_b; a.vsh = p->v_stride_h; a.vsn = p->v_stride_n;
+  a.osb = p->o_stride_b; a.osh = p->o_stride_h; a.osn = p->o_stride_n;
+  a.dosb = p->do_stride_b; a.dosh = p->do_stride_h; a.dosn = p->do_stride_n;
+  a.dqsb = p->dq_stride_b; a.dqsh = p->dq_stride_h; a.dqsn = p->dq_stride_n;
+  a.dksb = p->dk_stride_b; a.dksh = p->dk_stride_h; a.dksn = p->dk_stride_n;
+  a.dvsb = p->dv_stride_b; a.dvsh = p->dv_stride_h; a.dvsn = p->dv_stride_n;
+  a.stats = static_cast<float*>(p->workspace);
+  a.n = (int)p->seq_len;
+  a.nk = (int)bwd_kv_rows(p);
+  a.diag = p->causal == FA_CAUSAL_BOTTOM_RIGHT ? a.nk - a.n : 0;
+  a.hq = (int)p->heads_q;
+  a.group = (int)(p->heads_q / p->heads_kv);
+  a.c2 = p->scale * 1.4426950408889634f;
+  a.scale = p->scale;
+  fa::launch_backward(a, (int)p->batch, (int)p->head_dim, p->causal != FA_CAUSAL_NONE,
+                      p->dtype == FA_DTYPE_BF16, reinterpret_cast<hipStream_t>(p->stream));
+  return check_launch();
+}
+
+int64_t fa_sm75_backward_workspace_size(const fa_bwd_params* p) {
+  if (p == nullptr || p->batch < 0 || p->heads_q < 0 || p->seq_len < 0) return 0;
+  return fa::bwd_workspace_bytes(p->batch, p->heads_q, p->seq_len);
 }
 
 const char* fa_sm75_last_error(void) { return g_last_error; }

@@ -116,6 +116,60 @@ DecodePlan plan_decode(const FwdArgs& a, int batch, int head_dim, bool causal,
 int launch_decode_forward(const FwdArgs& a, const DecodePlan& plan, int head_dim, bool causal,
                           void* workspace, hipStream_t stream);
 
+// ---- Backward (fa_bwd.hip, fa_bwd_kernel.h) --------------------------------
+// Kernel arguments of the three backward kernels (passed by value).  The
+// grid-plan fields carry the names block_work reads.
+struct BwdArgs {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* v;
+  const _Float16* o;
+  const _Float16* dout;
+  const float* lse;  // [B*Hq, N] natural-log row LSE of the forward
+  _Float16* dq;
+  _Float16* dk;
+  _Float16* dv;
+  int64_t qsb, qsh, qsn;
+  int64_t ksb, ksh, ksn;
+  int64_t vsb, vsh, vsn;
+  int64_t osb, osh, osn;
+  int64_t dosb, dosh, dosn;
+  int64_t dqsb, dqsh, dqsn;
+  int64_t dksb, dksh, dksn;
+  int64_t dvsb, dvsh, dvsn;
+  // Workspace: per (b, query head) and 64-row query tile, 64 floats
+  // lse * log2(e) (+inf for rows past N and rows that see no key), then 64
+  // floats rowsum(dO * O) (0 past N).
+  float* stats;
+  int n;       // query rows
+  int nk;      // key/value rows
+  int diag;    // causal: key j visible to query i iff j <= i + diag
+  int hq;      // query heads
+  int group;   // heads_q / heads_kv
+  int qtiles;  // ceil(n / 64)
+  float c2;    // scale * log2(e), signed
+  float scale;
+  // grid plan (launcher)
+  int num_qblocks;  // dQ kernel: ceil(n / 128)
+  int units;        // batch * heads_kv
+  int xcds;         // 8 when units divide evenly over the XCDs, else 1
+  int items;        // dQ kernel work items
+  int pair_half;    // always 0 (no CU pairing)
+};
+constexpr int kBwdStatsTile = 64;    // query rows per stats record
+constexpr int kBwdBlockKeys = 128;   // keys per dK/dV workgroup
+constexpr int kBwdBlockRows = 128;   // query rows per dQ workgroup
+// Workspace bytes of a backward call.
+inline int64_t bwd_workspace_bytes(int64_t batch, int64_t heads_q, int64_t seq_len) {
+  return batch * heads_q * ((seq_len + kBwdStatsTile - 1) / kBwdStatsTile) *
+         (2 * kBwdStatsTile) * (int64_t)sizeof(float);
+}
+// Launches the stats, dK/dV and dQ kernels; all arguments validated.
+int launch_backward(const BwdArgs& a, int batch, int head_dim, bool causal, bool bf16,
+                    hipStream_t stream);
+template <int D, bool BF16>
+void launch_bwd(const BwdArgs& a, int batch, bool causal, hipStream_t stream);
+
 // Boolean mask -> bit rows (fa_mask.hip).
 int launch_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
                      int64_t cols, int64_t sb, int64_t sh, int64_t sq, int64_t sk,

@@ -44,6 +44,7 @@ struct Elem<false> {  // binary16
     return __builtin_amdgcn_fdot2(p, ones, acc, false);
   }
   static __device__ __forceinline__ _Float16 round(float x) { return (_Float16)x; }
+  static __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
 };
 template <>
 struct Elem<true> {  // bfloat16
@@ -60,6 +61,9 @@ struct Elem<true> {  // bfloat16
   }
   static __device__ __forceinline__ _Float16 round(float x) {
     return __builtin_bit_cast(_Float16, (__bf16)x);
+  }
+  static __device__ __forceinline__ float to_f32(_Float16 x) {
+    return __builtin_bit_cast(float, (unsigned)__builtin_bit_cast(unsigned short, x) << 16);
   }
 };
 
@@ -182,7 +186,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 struct Work {
   int b, hq, hkv, qb;
 };
-__device__ __forceinline__ Work block_work(const FwdArgs& a, int wg, bool causal) {
+// Args: FwdArgs, or BwdArgs for the backward's dQ kernel (same field names).
+template <class Args>
+__device__ __forceinline__ Work block_work(const Args& a, int wg, bool causal) {
   const int x = wg % a.xcds;
   int p = wg / a.xcds;
   if (a.pair_half > 0 && p >= a.pair_half) p = a.items / a.xcds - 1 + a.pair_half - p;

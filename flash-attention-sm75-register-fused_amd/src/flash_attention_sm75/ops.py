@@ -159,3 +159,72 @@ def flash_attention_forward_ex(Q, K, V, causal=False, scale=None, return_lse=Fal
     o, lse = _C.flash_attention_forward_ex(Q, K, V, code, float(scale), bool(return_lse),
                                            attn_mask)
     return (o, lse) if return_lse else o
+
+
+class FlashAttentionFunction(torch.autograd.Function):
+    """Differentiable fused attention: the MFMA forward (which also returns the
+    row LSE), then the MFMA backward from the saved Q, K, V, O and LSE.
+
+    No reference counterpart: the reference's Function is forward-only
+    (reference ops.py:47-52), and so is FlashAttentionSM75Function here.
+    """
+
+    @staticmethod
+    def forward(ctx, Q, K, V, code, scale):
+        O, LSE = _C.flash_attention_forward_ex(Q, K, V, code, scale, True, None)
+        ctx.save_for_backward(Q, K, V, O, LSE)
+        ctx.code = code
+        ctx.scale = scale
+        return O
+
+    @staticmethod
+    def backward(ctx, dO):
+        Q, K, V, O, LSE = ctx.saved_tensors
+        dQ, dK, dV = _C.flash_attention_backward(dO, Q, K, V, O, LSE, ctx.code, ctx.scale)
+        return dQ, dK, dV, None, None
+
+
+def flash_attention(Q, K, V, causal=False, scale=None):
+    """Fused attention with a backward pass (training).
+
+    Same inputs as :func:`flash_attention_forward_ex` (fp16 or bf16, grouped
+    K/V heads, N_q != N_k, either causal alignment), no ``attn_mask``.  When
+    autograd records the call, the backward computes dQ, dK and dV with the
+    fused MFMA kernels (deterministic; for grouped heads dK and dV sum over
+    each KV head's query heads).  No reference counterpart.
+
+    Returns:
+        O [B, H_q, N_q, D] in Q's dtype.
+    """
+    head_dim = _check_inputs(Q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    try:
+        code = _CAUSAL_CODES[causal]
+    except (KeyError, TypeError):
+        raise ValueError(
+            f"causal must be False, True, 'top_left' or 'bottom_right', got {causal!r}"
+        ) from None
+    _check_gqa_heads(Q, K)
+    if torch.is_grad_enabled() and (Q.requires_grad or K.requires_grad or V.requires_grad):
+        return FlashAttentionFunction.apply(Q, K, V, code, float(scale))
+    return _C.flash_attention_forward_ex(Q, K, V, code, float(scale), False, None)[0]
+
+
+def flash_attention_backward(dO, Q, K, V, O, LSE, causal=False, scale=None):
+    """Gradients (dQ, dK, dV) of ``O = flash_attention_forward_ex(Q, K, V,
+    causal, scale)`` given dO and that call's LSE (``return_lse=True``).
+
+    No reference counterpart.  Deterministic; fp16 or bf16 like the inputs.
+    """
+    head_dim = _check_inputs(Q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    try:
+        code = _CAUSAL_CODES[causal]
+    except (KeyError, TypeError):
+        raise ValueError(
+            f"causal must be False, True, 'top_left' or 'bottom_right', got {causal!r}"
+        ) from None
+    _check_gqa_heads(Q, K)
+    return _C.flash_attention_backward(dO, Q, K, V, O, LSE, code, float(scale))

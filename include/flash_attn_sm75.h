@@ -172,7 +172,69 @@ enum fa_kernel_policy {
 };
 int fa_sm75_set_kernel_policy(int policy); /* FA_OK or FA_ERR_INVALID_ARGUMENT */
 int fa_sm75_get_kernel_policy(void);
-#define FA_SM75_ABI_VERSION 3
+
+/* ---- Backward ------------------------------------------------------------
+ * Gradients dQ, dK, dV of O = softmax(scale * Q K^T + causal mask) V from
+ * dO = dL/dO, the forward's O and its fp32 row LSE (fa_fwd_params.lse).  No
+ * reference counterpart: the reference's autograd Function raises
+ * NotImplementedError in backward (src/flash_attention_sm75/ops.py:47-52);
+ * this is the pass the reference names as future work (reference
+ * DESIGN.md:155-163).
+ * Shapes and strides as in fa_fwd_params (head_dim contiguous; strides
+ * multiples of 8 elements); dQ, dO and O are [B, Hq, N, D], dK and dV
+ * [B, Hkv, Nk, D] (for grouped heads each KV head's gradient sums over its
+ * query heads).  P and dS are rounded to the element type before the
+ * products that take them; sums are fp32.  Deterministic: the same inputs
+ * give bitwise the same gradients.  No explicit mask. */
+typedef struct fa_bwd_params {
+  const fa_half* q;     /* [B, Hq,  N,  D] */
+  const fa_half* k;     /* [B, Hkv, Nk, D] */
+  const fa_half* v;     /* [B, Hkv, Nk, D] */
+  const fa_half* o;     /* [B, Hq,  N,  D] forward output */
+  const fa_half* dout;  /* [B, Hq,  N,  D] dL/dO */
+  const float* lse;     /* [B, Hq, N] contiguous fp32 natural-log row LSE of
+                           the forward (-inf: the row sees no key) */
+  fa_half* dq;          /* [B, Hq,  N,  D] output */
+  fa_half* dk;          /* [B, Hkv, Nk, D] output */
+  fa_half* dv;          /* [B, Hkv, Nk, D] output */
+  int64_t batch;
+  int64_t heads_q;
+  int64_t heads_kv;
+  int64_t seq_len;      /* N */
+  int64_t seq_len_kv;   /* Nk; 0 means Nk = seq_len */
+  int64_t head_dim;     /* 64 or 128 */
+  int64_t q_stride_b, q_stride_h, q_stride_n;
+  int64_t k_stride_b, k_stride_h, k_stride_n;
+  int64_t v_stride_b, v_stride_h, v_stride_n;
+  int64_t o_stride_b, o_stride_h, o_stride_n;
+  int64_t do_stride_b, do_stride_h, do_stride_n;
+  int64_t dq_stride_b, dq_stride_h, dq_stride_n;
+  int64_t dk_stride_b, dk_stride_h, dk_stride_n;
+  int64_t dv_stride_b, dv_stride_h, dv_stride_n;
+  float scale;          /* the forward's softmax scale */
+  int causal;           /* an fa_causal value (the forward's) */
+  int dtype;            /* an fa_dtype */
+  void* stream;         /* hipStream_t; NULL selects the default stream */
+  void* workspace;      /* device scratch of at least
+                           fa_sm75_backward_workspace_size() bytes, 16-byte
+                           aligned (required); calls that share one race */
+  int64_t workspace_bytes;
+} fa_bwd_params;
+
+/* Fills contiguous strides for every tensor of *p from its sizes. */
+void fa_sm75_set_contiguous_bwd_strides(fa_bwd_params* p);
+
+/* Backward: three kernels on p->stream (per-row statistics into the
+ * workspace, then dK/dV, then dQ).  Asynchronous; validates every argument
+ * before touching the device.  Returns FA_OK or an fa_status. */
+int fa_sm75_backward(const fa_bwd_params* p);
+
+/* Workspace bytes fa_sm75_backward needs: 512 per (batch, query head, 64
+ * query rows), from batch, heads_q and seq_len alone (0 if one is negative
+ * or p is NULL). */
+int64_t fa_sm75_backward_workspace_size(const fa_bwd_params* p);
+
+#define FA_SM75_ABI_VERSION 4
 
 /* ---- Reference launcher signatures ------------------------------------ */
 

@@ -5,6 +5,8 @@ __graft_entry__.smoke() and bench.py's cpu_baseline leg, never by the product.
 
 Reference anchors
   attention_reference  -> reference src/reference/attention_ref.py:10-45
+  attention_backward_f64 -> gradient of that math (the reference's backward
+                          raises: src/flash_attention_sm75/ops.py:47-52)
   expand_kv_for_gqa    -> reference src/flash_attention_sm75/ops.py:6-27
   check_correctness    -> reference src/reference/correctness.py:8-37
   flops                -> reference benchmarks/benchmark_attention.py:78-82
@@ -204,6 +206,50 @@ def attention_f64(Q, K, V, causal=False, scale=None, attn_mask=None):
     E = np.exp(S - m)
     tot = E.sum(axis=-1, keepdims=True)
     return np.matmul(E / np.where(tot > 0, tot, 1.0), v)
+
+
+def attention_backward_f64(Q, K, V, dO, causal=False, scale=None):
+    """Gradients (dQ, dK, dV) of attention_f64's O in float64, closed form.
+
+    No reference counterpart: the reference's autograd backward raises
+    (ops.py:47-52).  This is the textbook gradient of the math path of
+    attention_ref.py:24-45, O = softmax(scale Q K^T + mask) V:
+      P = softmax(S), dV = P^T dO, dP = dO V^T,
+      dS = P o (dP - rowsum(dP o P)), dQ = scale dS K, dK = scale dS^T Q.
+    A KV head shared by a group of query heads gets the sum of the group's
+    gradients (the adjoint of the repeat_interleave at ops.py:24-26).  Rows
+    that see no key have P = 0 and contribute nothing.
+    """
+    Q = np.asarray(Q)
+    K = np.asarray(K)
+    V = np.asarray(V)
+    B, Hq, N, D = Q.shape
+    Hkv, Nk = K.shape[1], K.shape[2]
+    Ke, Ve = expand_kv_for_gqa(Q, K, V)
+    if scale is None:
+        scale = default_scale(D)
+    q = Q.astype(np.float64)
+    k = Ke.astype(np.float64)
+    v = Ve.astype(np.float64)
+    do = np.asarray(dO).astype(np.float64)
+    S = np.matmul(q, np.swapaxes(k, -1, -2)) * float(scale)
+    mask = causal_mask(N, Nk, causal)
+    if mask is not None:
+        S[..., mask] = -np.inf
+    m = S.max(axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
+    E = np.exp(S - m)
+    tot = E.sum(axis=-1, keepdims=True)
+    P = E / np.where(tot > 0, tot, 1.0)
+    dv = np.matmul(np.swapaxes(P, -1, -2), do)
+    dP = np.matmul(do, np.swapaxes(v, -1, -2))
+    dS = P * (dP - (dP * P).sum(axis=-1, keepdims=True))
+    dq = float(scale) * np.matmul(dS, k)
+    dk = float(scale) * np.matmul(np.swapaxes(dS, -1, -2), q)
+    g = Hq // Hkv
+    dk = dk.reshape(B, Hkv, g, Nk, D).sum(axis=2)
+    dv = dv.reshape(B, Hkv, g, Nk, D).sum(axis=2)
+    return dq, dk, dv
 
 
 def check_correctness(output, reference, name="", atol=1e-2, rtol=1e-2):

@@ -28,3 +28,22 @@ class Params(ctypes.Structure):
 
 FA_CAUSAL_NONE, FA_CAUSAL_TOP_LEFT, FA_CAUSAL_BOTTOM_RIGHT = 0, 1, 2
 FA_DTYPE_FP16, FA_DTYPE_BF16 = 0, 1
+
+
+def _strides(*names):
+    return [(f"{n}_stride_{d}", ctypes.c_int64) for n in names for d in ("b", "h", "n")]
+
+
+class BwdParams(ctypes.Structure):
+    """fa_bwd_params."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p), ("dout", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p), ("dk", ctypes.c_void_p), ("dv", ctypes.c_void_p),
+        ("batch", ctypes.c_int64), ("heads_q", ctypes.c_int64), ("heads_kv", ctypes.c_int64),
+        ("seq_len", ctypes.c_int64), ("seq_len_kv", ctypes.c_int64), ("head_dim", ctypes.c_int64),
+    ] + _strides("q", "k", "v", "o", "do", "dq", "dk", "dv") + [
+        ("scale", ctypes.c_float), ("causal", ctypes.c_int), ("dtype", ctypes.c_int),
+        ("stream", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
+    ]

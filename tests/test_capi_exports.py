@@ -49,7 +49,8 @@ def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("fa_sm75_forward", "fa_sm75_naive_forward", "fa_sm75_last_error",
               "fa_sm75_status_string", "fa_sm75_abi_version", "fa_sm75_set_contiguous_strides",
-              "fa_sm75_workspace_size", "fa_sm75_pack_mask",
+              "fa_sm75_workspace_size", "fa_sm75_pack_mask", "fa_sm75_backward",
+              "fa_sm75_backward_workspace_size", "fa_sm75_set_contiguous_bwd_strides",
               "launch_flash_attention_forward", "launch_flash_attention_forward_scalar",
               "launch_flash_attention_forward_wmma_qk", "launch_naive_attention"):
         assert n in names, n
@@ -208,7 +209,7 @@ def test_mask_param_validation(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_sm75_abi_version() == 3
+    assert lib.fa_sm75_abi_version() == 4
 
 
 def test_kernel_policy_switch(lib):

@@ -1,0 +1,188 @@
+"""The backward kernels (dQ, dK, dV) against the float64 oracle (needs a GPU).
+
+No reference counterpart: the reference's backward raises
+(src/flash_attention_sm75/ops.py:47-52).  The oracle
+(attention_backward_f64, pinned in test_oracle_backward.py) is the exact
+gradient of the same fp16/bf16 inputs.  The kernels round P and dS to the
+element type before the products that take them (as the forward rounds P),
+use the rounded forward output in rowsum(dO o O), and round the gradients;
+each of those is a relative 2^-11 (binary16) or 2^-8 (bfloat16) error on
+terms of mixed sign.  Bar, per gradient tensor G against its oracle R:
+    |G - R| <= ATOL * max|R| + RTOL * |R|   elementwise,
+binary16 ATOL = 2e-3, RTOL = 1e-2 (the forward's bar, with the absolute
+term relative to the gradient's scale); bfloat16 ATOL = 1e-2, RTOL = 4e-2
+(the 8x coarser rounding).  Observed: up to 0.2 (binary16) and 0.35
+(bfloat16) of the bar; max|R| is floored at 1e-2, since a gradient
+that is exactly zero (dQ with a single key) comes out as rounding noise of
+the P(dP - rowsum) cancellation.  At sizes the oracle cannot reach, two exact
+identities of the gradient are checked instead: the keys' dK rows sum to
+zero, and the keys' dV rows sum to the dO rows of the group's queries.
+"""
+import numpy as np
+import pytest
+import torch
+
+import flash_attn_sm75_cuda as _C
+from flash_attention_sm75 import (flash_attention, flash_attention_backward,
+                                  flash_attention_forward, flash_attention_forward_ex)
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+BAR = {torch.float16: (2e-3, 1e-2), torch.bfloat16: (1e-2, 4e-2)}
+CODE = {False: 0, True: 1, "bottom_right": 2}
+
+
+def seeded(shape, seed, dtype=torch.float16):
+    g = torch.Generator("cpu").manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype)
+
+
+def npf(t):
+    return t.float().cpu().numpy()
+
+
+def run_backward(q, k, v, do, causal, device, scale=None):
+    qd, kd, vd, dod = (t.to(device) for t in (q, k, v, do))
+    o, lse = flash_attention_forward_ex(qd, kd, vd, causal=causal, scale=scale, return_lse=True)
+    grads = flash_attention_backward(dod, qd, kd, vd, o, lse, causal=causal, scale=scale)
+    torch.cuda.synchronize()
+    return grads
+
+
+def assert_grads(grads, want, dtype, label):
+    atol, rtol = BAR[dtype]
+    for name, g, w in zip(("dQ", "dK", "dV"), grads, want):
+        g = npf(g)
+        scale = max(float(np.abs(w).max()) if w.size else 0.0, 1e-2)
+        err = np.abs(g - w)
+        worst = float((err / (atol * scale + rtol * np.abs(w) + 1e-30)).max()) if w.size else 0.0
+        print(f"  {label} {name}: max_abs={err.max() if err.size else 0:.3e} "
+              f"max|R|={scale:.3e} worst/bar={worst:.3f}", flush=True)
+        assert np.isfinite(g).all(), name
+        assert worst <= 1.0, (name, worst)
+
+
+CASES = [
+    # B, Hq, Hkv, Nq, Nk, D, causal
+    (1, 2, 2, 128, 128, 64, False),
+    (1, 2, 2, 128, 128, 128, True),
+    (1, 4, 2, 200, 200, 128, True),      # ragged tail, GQA 2:1
+    (2, 8, 2, 333, 333, 64, True),       # GQA 4:1, odd length
+    (2, 3, 3, 1, 1, 128, False),         # single row
+    (1, 4, 1, 513, 513, 64, False),      # MQA, one row past a block
+    (1, 4, 4, 100, 260, 128, "bottom_right"),
+    (1, 2, 1, 300, 77, 64, "bottom_right"),  # rows that see no key
+    (1, 2, 2, 70, 300, 128, True),       # top-left with Nq < Nk: keys no query sees
+    (1, 8, 8, 1024, 1024, 128, True),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Nq,Nk,D,causal", CASES)
+def test_backward_matches_oracle(device, B, Hq, Hkv, Nq, Nk, D, causal):
+    print(f"[bwd] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} causal={causal}", flush=True)
+    q, k, v = seeded((B, Hq, Nq, D), 1), seeded((B, Hkv, Nk, D), 2), seeded((B, Hkv, Nk, D), 3)
+    do = seeded((B, Hq, Nq, D), 4)
+    grads = run_backward(q, k, v, do, causal, device)
+    want = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=CODE[causal])
+    assert_grads(grads, want, torch.float16, f"Nq{Nq} Nk{Nk} D{D}")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Nq,Nk,D,causal", [
+    (1, 4, 2, 200, 200, 128, True),
+    (2, 4, 1, 150, 150, 64, False),
+    (1, 2, 2, 90, 170, 64, "bottom_right"),
+])
+def test_backward_bf16(device, B, Hq, Hkv, Nq, Nk, D, causal):
+    print(f"[bwd bf16] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} causal={causal}", flush=True)
+    bf = torch.bfloat16
+    q, k, v = seeded((B, Hq, Nq, D), 5, bf), seeded((B, Hkv, Nk, D), 6, bf), seeded((B, Hkv, Nk, D), 7, bf)
+    do = seeded((B, Hq, Nq, D), 8, bf)
+    grads = run_backward(q, k, v, do, causal, device)
+    assert all(g.dtype == bf for g in grads)
+    want = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=CODE[causal])
+    assert_grads(grads, want, bf, f"bf16 Nq{Nq} Nk{Nk} D{D}")
+
+
+def test_scale_values(device):
+    """Non-default, negative and zero softmax scales."""
+    q, k, v = seeded((1, 2, 96, 64), 9), seeded((1, 2, 96, 64), 10), seeded((1, 2, 96, 64), 11)
+    do = seeded((1, 2, 96, 64), 12)
+    for scale in (0.3, -0.125, 0.0):
+        print(f"[bwd scale] {scale}", flush=True)
+        grads = run_backward(q, k, v, do, True, device, scale=scale)
+        want = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=1, scale=scale)
+        assert_grads(grads, want, torch.float16, f"scale {scale}")
+
+
+def test_autograd_function(device):
+    """flash_attention under autograd: its gradients are the backward op's,
+    and the reference-named forward keeps its forward-only contract."""
+    print("[bwd autograd]", flush=True)
+    B, Hq, Hkv, N, D = 2, 8, 2, 300, 128
+    q, k, v = seeded((B, Hq, N, D), 13), seeded((B, Hkv, N, D), 14), seeded((B, Hkv, N, D), 15)
+    do = seeded((B, Hq, N, D), 16)
+    leaves = [t.to(device).requires_grad_() for t in (q, k, v)]
+    o = flash_attention(*leaves, causal=True)
+    o.backward(do.to(device))
+    direct = run_backward(q, k, v, do, True, device)
+    for leaf, d in zip(leaves, direct):
+        assert torch.equal(leaf.grad, d)
+    want = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=1)
+    assert_grads([l.grad for l in leaves], want, torch.float16, "autograd")
+    # the reference's Function still raises in backward (reference tests/test_api.py:38)
+    x = [t.to(device).requires_grad_() for t in (q, k, v)]
+    with pytest.raises(NotImplementedError, match="Backward pass is not implemented"):
+        flash_attention_forward(*x, causal=True).sum().backward()
+
+
+def test_deterministic_and_strided(device):
+    """Bitwise-repeatable; strided [B, N, H, D] views give the same gradients."""
+    print("[bwd strided]", flush=True)
+    B, Hq, Hkv, N, D = 2, 8, 4, 257, 64
+    q, k, v = seeded((B, Hq, N, D), 17), seeded((B, Hkv, N, D), 18), seeded((B, Hkv, N, D), 19)
+    do = seeded((B, Hq, N, D), 20)
+    a = run_backward(q, k, v, do, True, device)
+    b = run_backward(q, k, v, do, True, device)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    views = [t.to(device).transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v, do)]
+    assert not views[0].is_contiguous()
+    o, lse = flash_attention_forward_ex(*views[:3], causal=True, return_lse=True)
+    c = flash_attention_backward(views[3], *views[:3], o, lse, causal=True)
+    torch.cuda.synchronize()
+    for x, y in zip(a, c):
+        assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_key_sum_identities_at_size(device, causal):
+    """B=1 Hq=16 Hkv=4 N=4096 D=128: sum_j dK_j = 0 and sum_j dV_j equals the
+    group's sum of dO rows, within the rounding of the fp16 gradients."""
+    print(f"[bwd identities] causal={causal}", flush=True)
+    B, Hq, Hkv, N, D = 1, 16, 4, 4096, 128
+    q, k, v = (seeded(s, i) for s, i in (((B, Hq, N, D), 21), ((B, Hkv, N, D), 22),
+                                          ((B, Hkv, N, D), 23)))
+    do = seeded((B, Hq, N, D), 24)
+    dq, dk, dv = (g.double() for g in run_backward(q, k, v, do, causal, device))
+    r_k = (dk.sum(2).abs().amax() / dk.abs().sum(2).amax()).item()
+    do_g = do.to(device).double().reshape(B, Hkv, Hq // Hkv, N, D).sum(dim=(2, 3))
+    r_v = ((dv.sum(2) - do_g).abs().amax() / dv.abs().sum(2).amax()).item()
+    print(f"  sum dK residual {r_k:.2e}, sum dV residual {r_v:.2e}", flush=True)
+    assert r_k < 2e-3 and r_v < 2e-3
+    assert torch.isfinite(dq).all()
+
+
+def test_empty_and_degenerate(device):
+    """No query rows: dK = dV = 0; zero batch: empty gradients."""
+    print("[bwd empty]", flush=True)
+    k = seeded((1, 2, 50, 64), 25).to(device)
+    q = torch.empty(1, 4, 0, 64, dtype=torch.float16, device=device)
+    o = torch.empty_like(q)
+    lse = torch.empty(1, 4, 0, dtype=torch.float32, device=device)
+    dq, dk, dv = _C.flash_attention_backward(o, q, k, k, o, lse, 0, 0.125)
+    torch.cuda.synchronize()
+    assert dq.shape == q.shape and torch.count_nonzero(dk) == 0 and torch.count_nonzero(dv) == 0
+    z = torch.empty(0, 2, 8, 64, dtype=torch.float16, device=device)
+    out = _C.flash_attention_backward(z, z, z, z, z, torch.empty(0, 2, 8, device=device), 1, 0.1)
+    assert all(t.numel() == 0 for t in out)
