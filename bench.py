@@ -2,7 +2,7 @@
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
                   [--no-cpu-baseline] [--no-gemm-ceiling] [--all] [--decode] [--hf]
-                  [--shape B,Hq,Hkv,N,D,causal]
+                  [--shape B,Hq,Hkv,N,D,causal] [--no-backward]
 
 A step is one fused forward over one batch of synthetic input (the hot path:
 flash_attention_sm75.flash_attention_forward -> flash_attn_sm75_cuda ->
@@ -24,7 +24,9 @@ Printed: ONE JSON line on stdout (rank 0).  Besides the driver's keys it holds
                 operands timed in the same run, the rate the MFMA pipes hold
                 under the board's power limit, and the kernel's share of it;
   cpu_baseline  the reference math path (restated with torch on the host
-                CPU) timed on a bounded sample of the same workload.
+                CPU) timed on a bounded sample of the same workload;
+  backward      the backward pass (dQ, dK, dV) on the same workload: its
+                average time and TFLOPS at 2.5x the forward's FLOP count.
 Diagnostics go to stderr.
 """
 import argparse
@@ -258,6 +260,35 @@ def time_sdpa_decode_call(keys, n=200):
     return out
 
 
+def time_backward(cfg, steps=10, warmup=3):
+    """Average time of one flash_attention_backward call (stats, dK/dV and dQ
+    kernels) on the workload's shape, HIP events on the launch stream around
+    the timed calls; inputs, O, LSE and dO resident in HBM."""
+    import torch
+
+    from flash_attention_sm75 import flash_attention_backward, flash_attention_forward_ex
+
+    B, Hq, Hkv, N, D, causal, std, _ = CONFIGS[cfg]
+    dev = torch.device("cuda", 0)
+    g = torch.Generator("cpu").manual_seed(11)
+    q = (torch.randn(B, Hq, N, D, generator=g) * std).half().to(dev)
+    k = (torch.randn(B, Hkv, N, D, generator=g) * std).half().to(dev)
+    v = (torch.randn(B, Hkv, N, D, generator=g) * std).half().to(dev)
+    do = torch.randn(B, Hq, N, D, generator=g).half().to(dev)
+    o, lse = flash_attention_forward_ex(q, k, v, causal=causal, return_lse=True)
+    for _ in range(warmup):
+        flash_attention_backward(do, q, k, v, o, lse, causal=causal)
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(steps):
+        flash_attention_backward(do, q, k, v, o, lse, causal=causal)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
 def time_hf(prompt_len=4096, decode_steps=32):
     """Random-init Qwen2-0.5B-shaped model (no weights can be downloaded):
     prefill and teacher-forced KV-cache decode, unpatched vs patched SDPA."""
@@ -333,6 +364,8 @@ def main():
                          "(the kernel is power-limited: less data toggling, higher clock)")
     ap.add_argument("--policy", type=int, default=0, choices=(0, 1, 2),
                     help="kernel policy: 0 auto, 1 = 128-row (4-wave), 2 = 256-row (8-wave)")
+    ap.add_argument("--no-backward", action="store_true",
+                    help="skip timing the backward pass on the same workload")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise copy of 256 MiB (known HBM bytes) "
                          "to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
@@ -420,6 +453,19 @@ def main():
         }
         log(f"[gemm-ceiling] {ceiling}")
 
+    backward = None
+    if not args.no_backward and args.data == "randn":
+        bms = time_backward(cfg)
+        backward = {
+            "ms": round(bms, 5),
+            "tflops": round(2.5 * F / (bms * 1e-3) / 1e12, 2),
+            "flop": int(2.5 * F),
+            "flop_convention": "2.5x the forward's (5 matrix products: QK^T, dP, dV, dK, dQ); "
+                               "the kernels execute 3.5x (dQ recomputes QK^T and dP)",
+            "kernels": "fa_bwd_stats + fa_bwd_dkdv + fa_bwd_dq, deterministic, fp16",
+        }
+        log(f"[{cfg} backward] {backward}")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.cpu_budget)
@@ -458,6 +504,7 @@ def main():
             "sustained_mfma": ceiling,
         },
         "cpu_baseline": cpu,
+        "backward": backward,
     }
     print(json.dumps(line), flush=True)
 

@@ -322,9 +322,11 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
 // ---- dQ ----------------------------------------------------------------------
 // The forward's work decomposition (block_work; causal: largest block
 // first): wave w owns query rows q0 + 32w .. +32 and walks the 64-key tiles
-// its block can see, K and V tiles double buffered through LDS.
+// its block can see, K and V tiles double buffered through LDS.  Two
+// workgroups per CU (238 VGPRs, 80 KiB of LDS each): measured 26% faster
+// than one on the C4 training shape.
 template <int D, bool CAUSAL, bool BF16>
-__global__ void __launch_bounds__(256, 1) fa_bwd_dq_kernel(const BwdArgs a) {
+__global__ void __launch_bounds__(256, 2) fa_bwd_dq_kernel(const BwdArgs a) {
   using L = Lds<D>;
   using E = Elem<BF16>;
   constexpr int KK = D / 16;

@@ -20,12 +20,14 @@ without changing results:
   * grouped K/V heads go to the kernel as they are (no repeat_interleave);
   * bfloat16 calls (most current models' dtype) run on the kernel's bfloat16
     instances; other dtypes, and mixed ones, fall back;
-  * calls that need gradients fall back (the kernel is forward-only).
+  * calls that need gradients (training) run on :func:`flash_attention`,
+    whose backward is the fused dQ/dK/dV kernels; with a boolean mask they
+    fall back (the backward takes no mask).
 """
 import torch
 import torch.nn.functional as F
 
-from .ops import flash_attention_forward_ex
+from .ops import flash_attention, flash_attention_forward_ex
 
 _original_sdpa = F.scaled_dot_product_attention
 _patch_active = False
@@ -70,10 +72,14 @@ def _fallback_reason(query, key, value, attn_mask, dropout_p, is_causal, kwargs)
         return "empty_kv"
     if set(kwargs) - {"enable_gqa"}:
         return "unsupported_kwargs"
-    if torch.is_grad_enabled() and (query.requires_grad or key.requires_grad
-                                    or value.requires_grad):
-        return "requires_grad"
+    if attn_mask is not None and _needs_grad(query, key, value):
+        return "requires_grad"  # the backward kernels take no mask
     return None
+
+
+def _needs_grad(query, key, value):
+    return torch.is_grad_enabled() and (query.requires_grad or key.requires_grad
+                                        or value.requires_grad)
 
 
 def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
@@ -86,6 +92,8 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
         return _original_sdpa(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
                               is_causal=is_causal, scale=scale, **kwargs)
     _stats["flash"] += 1
+    if _needs_grad(query, key, value):
+        return flash_attention(query, key, value, causal=bool(is_causal), scale=scale)
     return flash_attention_forward_ex(query, key, value, causal=bool(is_causal), scale=scale,
                                       attn_mask=attn_mask)
 
