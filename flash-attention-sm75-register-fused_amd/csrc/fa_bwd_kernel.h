@@ -145,8 +145,19 @@ __global__ void __launch_bounds__(256) fa_bwd_stats_kernel(const BwdArgs a) {
 // ---- dK, dV ------------------------------------------------------------------
 // Step s of a workgroup: query head hkv * group + s / per_head, query tile
 // qt_begin + s % per_head (causal: the first tile with a query that sees one
-// of the block's keys).  Tiles are double buffered: step s loads step s+1's
-// Q, dO and stats while it computes, then one barrier.
+// of the block's keys), two 32-query sub-tiles each.
+//
+// One wave per SIMD (128 accumulator, 64 operand VGPRs per lane; 123 KiB of
+// LDS), so the wave has to hide its own latencies: the loop is software
+// pipelined and hand ordered, as the forward's.  Phase (s, t) issues, one
+// MFMA per slot, the S and dP products of the *next* sub-tile, then the dV
+// and dK products of sub-tile (s, t); the softmax of (s, t) -- exp, dS, the
+// packing into B operands -- is spread over the first slots, and every LDS
+// operand read runs a few MFMAs ahead of its use.  Q/dO tiles (and their
+// stats) are triple buffered: the barrier between the two phases of step s
+// releases the buffer of step s-1, which then receives step s+2.
+typedef float float4v __attribute__((ext_vector_type(4)));
+
 template <int D, bool CAUSAL, bool BF16>
 __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
   using L = Lds<D>;
@@ -154,13 +165,20 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
   constexpr int KK = D / 16;
   constexpr int MT = D / 32;
   constexpr int SEGQ = L::Segs / 4;
+  constexpr int NSD = 2 * KK;  // S and dP MFMAs of a sub-tile
+  constexpr int NGR = 4 * MT;  // dV and dK MFMAs of a sub-tile
+  constexpr int PFR = 3;       // row-operand reads run this many MFMAs ahead
+  constexpr int PFT = 2;       // transposing reads run this many MFMAs ahead
   __shared__ __attribute__((aligned(1024))) _Float16 q_lds0[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 q_lds1[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 q_lds2[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 d_lds0[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 d_lds1[L::Tile];
+  __shared__ __attribute__((aligned(1024))) _Float16 d_lds2[L::Tile];
   // 128 floats of stats per tile; a whole-wave direct load writes 1 KB.
   __shared__ __attribute__((aligned(1024))) float s_lds0[256];
   __shared__ __attribute__((aligned(1024))) float s_lds1[256];
+  __shared__ __attribute__((aligned(1024))) float s_lds2[256];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = (int)threadIdx.x & 63;
@@ -209,9 +227,34 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
     goff_q[s] = seg_offset<D>(wave + 4 * s, lane, a.qsn);
     goff_d[s] = seg_offset<D>(wave + 4 * s, lane, a.dosn);
   }
+  // Buffers by compile-time stage index.
+  auto qbuf = [&](auto st) -> _Float16* {
+    constexpr int S = decltype(st)::value % 3;
+    if constexpr (S == 0) return q_lds0;
+    else if constexpr (S == 1) return q_lds1;
+    else return q_lds2;
+  };
+  auto dbuf = [&](auto st) -> _Float16* {
+    constexpr int S = decltype(st)::value % 3;
+    if constexpr (S == 0) return d_lds0;
+    else if constexpr (S == 1) return d_lds1;
+    else return d_lds2;
+  };
+  auto sbuf = [&](auto st) -> float* {
+    constexpr int S = decltype(st)::value % 3;
+    if constexpr (S == 0) return s_lds0;
+    else if constexpr (S == 1) return s_lds1;
+    else return s_lds2;
+  };
+  auto qbase_of = [&](int s) {
+    const int h = s / per_head;
+    return (qt_begin + (s - h * per_head)) * kBwdStatsTile;
+  };
   // Direct loads of step s's Q and dO tiles (wave w: segments w, w+4, ..)
-  // and, by wave 0, its stats record.
-  auto issue = [&](int s, _Float16* qdst, _Float16* ddst, float* sdst) {
+  // and, by wave 0, its stats record, into the buffers of stage ST.
+  auto issue = [&](int s, auto st) {
+    _Float16* const qdst = qbuf(st);
+    _Float16* const ddst = dbuf(st);
     const int h = s / per_head;
     const int qt = qt_begin + (s - h * per_head);
     const int hq = hkv * a.group + h;
@@ -230,74 +273,180 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
       const __amdgpu_buffer_rsrc_t rs = make_rsrc(
           a.stats + ((int64_t)(b * a.hq + hq) * a.qtiles + qt) * (2 * kBwdStatsTile),
           2 * kBwdStatsTile * 4);
-      direct_load16(rs, (lds_void*)sdst, 16 * lane);
+      direct_load16(rs, (lds_void*)sbuf(st), 16 * lane);
     }
   };
 
   const TileReader<D> rd(lane);
-  const float c2 = a.c2;
-
-  auto step = [&](int s, auto par_t) {
-    constexpr int PAR = decltype(par_t)::value;
-    const _Float16* qc = PAR ? q_lds1 : q_lds0;
-    const _Float16* dc = PAR ? d_lds1 : d_lds0;
-    const float* sc = PAR ? s_lds1 : s_lds0;
-    if (s + 1 < steps) issue(s + 1, PAR ? q_lds0 : q_lds1, PAR ? d_lds0 : d_lds1,
-                             PAR ? s_lds0 : s_lds1);
-    const int h = s / per_head;
-    const int qbase = (qt_begin + (s - h * per_head)) * kBwdStatsTile;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      float16v sa = (float16v)0.0f, dpa = (float16v)0.0f;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) sa = E::mfma(rd.row(qc, t, kk), kf[kk], sa);
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) dpa = E::mfma(rd.row(dc, t, kk), vf[kk], dpa);
-      // Element i: query qbase + 32t + 8(i/4) + 4hi + i%4, key krow.
-      const bool need_mask = CAUSAL && kw + 31 > qbase + 32 * t + a.diag;
-      uint4v pp[2], pd[2];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 l4 = *(const float4*)(sc + 32 * t + 8 * g + 4 * hi);
-        const float4 d4 = *(const float4*)(sc + kBwdStatsTile + 32 * t + 8 * g + 4 * hi);
-        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-        const float dl[4] = {d4.x, d4.y, d4.z, d4.w};
-        float pv[4], dsv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * g + e;
-          float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i], c2, -lv[e]));
-          if (need_mask && krow > qbase + 32 * t + 8 * g + 4 * hi + e + a.diag) pe = 0.0f;
-          pv[e] = pe;
-          dsv[e] = pe * (dpa[i] - dl[e]);
-        }
-        put_pair<E>(pp, 0, 4 * g, pv[0], pv[1]);
-        put_pair<E>(pp, 0, 4 * g + 2, pv[2], pv[3]);
-        put_pair<E>(pd, 0, 4 * g, dsv[0], dsv[1]);
-        put_pair<E>(pd, 0, 4 * g + 2, dsv[2], dsv[3]);
-      }
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          dv[mt] = E::mfma(rd.tr(dc, 2 * t + h2, mt), __builtin_bit_cast(half8, pp[h2]), dv[mt]);
-          dk[mt] = E::mfma(rd.tr(qc, 2 * t + h2, mt), __builtin_bit_cast(half8, pd[h2]), dk[mt]);
-        }
+  // P = exp2(S c2 - lse2); c2 keeps its sign away from 0 (scale 0: uniform
+  // weights), so a score set to mval gives P = 0 exactly.
+  const float c2 = a.c2 != 0.0f ? a.c2 : 1e-30f;
+  const float mval = c2 > 0.0f ? -__builtin_inff() : __builtin_inff();
+  // Scores of sub-tile t of step s whose key is past the causal diagonal of
+  // their query (element i: query q0 + 8(i/4) + 4hi + i%4) -> mval.
+  auto mask_scores = [&](float16v& sv, int s, int t) {
+    if constexpr (CAUSAL) {
+      const int q0 = qbase_of(s) + 32 * t;
+      if (kw + 31 > q0 + a.diag) {
+        static_for<16>([&](auto i_c) {
+          constexpr int i = decltype(i_c)::value;
+          if (krow > q0 + 8 * (i >> 2) + 4 * hi + (i & 3) + a.diag) sv[i] = mval;
+        });
       }
     }
-    // This wave's loads for step s+1 have landed, and every wave is done
-    // reading the buffers that step s+1 refills for step s+2.
-    barrier_after_loads<0>();
   };
 
-  if (steps > 0) issue(0, q_lds0, d_lds0, s_lds0);
-  barrier_after_loads<0>();
-  int s = 0;
-  for (; s + 1 < steps; s += 2) {
-    step(s, std::integral_constant<int, 0>{});
-    step(s + 1, std::integral_constant<int, 1>{});
+  // S and dP of the current (index t) and next (1 - t) sub-tile.
+  float16v sb[2], db[2];
+
+  // Phase (s, T) on the buffers of stage B: HAS_NEXT -- the next sub-tile
+  // ((s, 1) or (s+1, 0), stage B or B+1) exists and its S, dP are computed.
+  auto phase = [&](int s, auto t_c, auto b_c, auto has_next_c) {
+    constexpr int T = decltype(t_c)::value;
+    constexpr int B = decltype(b_c)::value;
+    constexpr bool HAS_NEXT = decltype(has_next_c)::value;
+    constexpr int BN = T == 0 ? B : B + 1;  // stage of the next sub-tile
+    constexpr int TN = 1 - T;
+    constexpr int NS = HAS_NEXT ? NSD : 0;  // S/dP slots
+    constexpr int NBS = NS + NGR;           // slots
+    const _Float16* qc = qbuf(b_c);
+    const _Float16* dc = dbuf(b_c);
+    const float* sc = sbuf(b_c);
+    const _Float16* qn = qbuf(std::integral_constant<int, BN>{});
+    const _Float16* dn = dbuf(std::integral_constant<int, BN>{});
+
+    // Row statistics of this sub-tile's rows 32T + 8g + 4hi + 0..3, read a
+    // couple of slots before the first pair that needs them.
+    float4v l4[4], d4[4];
+    auto read_stats = [&](auto g_c) {
+      constexpr int g = decltype(g_c)::value;
+      l4[g] = *(const float4v*)(sc + 32 * T + 8 * g + 4 * hi);
+      d4[g] = *(const float4v*)(sc + kBwdStatsTile + 32 * T + 8 * g + 4 * hi);
+    };
+    uint4v pp[2], pd[2];  // P and dS as B operands of the two 16-query steps
+    half8 rf[NSD > 0 ? NSD : 1], tf[NGR];
+    // Row operand i of the next sub-tile: Q (even i) or dO (odd i), dims 16(i/2)..
+    auto read_row = [&](int i) -> half8 {
+      return rd.row((i & 1) ? dn : qn, TN, i >> 1);
+    };
+    // Transposed operand v: 16-query step h2 = v / (2 MT), output tile
+    // mt = (v / 2) % MT, dO^T (even v, for dV) or Q^T (odd v, for dK).
+    auto read_tr = [&](int v) -> half8 {
+      return rd.tr((v & 1) ? qc : dc, 2 * T + v / (2 * MT), (v >> 1) % MT);
+    };
+    auto softmax_pair = [&](auto p_c) {
+      constexpr int pr = decltype(p_c)::value;
+      constexpr int i = 2 * pr, g = i >> 2, e = i & 3;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sb[T][i], c2, -l4[g][e]));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sb[T][i + 1], c2, -l4[g][e + 1]));
+      const float s0 = p0 * (db[T][i] - d4[g][e]);
+      const float s1 = p1 * (db[T][i + 1] - d4[g][e + 1]);
+      pp[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, E::pack(p0, p1));
+      pd[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, E::pack(s0, s1));
+    };
+    // Pair pr feeds 16-query step pr / 4, whose first MFMA is in slot
+    // NS + (pr / 4) 2 MT; within a slot the MFMA goes first, so the pair must
+    // sit in an earlier slot (-1: before the slots).  Spread from slot 1 (the
+    // statistics reads land meanwhile).
+    constexpr auto pair_slot = [](int pr) constexpr {
+      const int spread = 1 + (pr * (NS + 2 * MT - 1)) / 8;
+      const int last_ok = NS + (pr / 4) * 2 * MT - 1;
+      return spread < last_ok ? spread : last_ok;
+    };
+    // Statistics group g (pairs 2g, 2g+1) is read at stats_slot(g).
+    constexpr auto stats_slot = [pair_slot](int g) constexpr {
+      const int s = pair_slot(2 * g) - 2;
+      return s < 0 ? -1 : s;
+    };
+    static_for<4>([&](auto g_c) {
+      if constexpr (stats_slot(decltype(g_c)::value) < 0) read_stats(g_c);
+    });
+    static_for<8>([&](auto p_c) {
+      if constexpr (pair_slot(decltype(p_c)::value) < 0) softmax_pair(p_c);
+    });
+    static_for<(PFR < NS ? PFR : NS)>([&](auto i_c) {
+      rf[decltype(i_c)::value] = read_row(decltype(i_c)::value);
+    });
+    static_for<NBS>([&](auto slot_c) {
+      constexpr int slot = decltype(slot_c)::value;
+      if constexpr (slot == (NS >= PFT ? NS - PFT : 0)) {
+        static_for<PFT>([&](auto v_c) { tf[decltype(v_c)::value] = read_tr(decltype(v_c)::value); });
+      }
+      if constexpr (slot >= NS && slot - NS + PFT < NGR) tf[slot - NS + PFT] = read_tr(slot - NS + PFT);
+      if constexpr (slot < NS) {
+        constexpr int i = slot, kk = i >> 1;
+        if constexpr (i + PFR < NS) rf[i + PFR] = read_row(i + PFR);
+        if constexpr ((i & 1) == 0)
+          sb[TN] = E::mfma(rf[i], kf[kk], kk == 0 ? (float16v)0.0f : sb[TN]);
+        else
+          db[TN] = E::mfma(rf[i], vf[kk], kk == 0 ? (float16v)0.0f : db[TN]);
+      } else {
+        constexpr int v = slot - NS, h2 = v / (2 * MT), mt = (v >> 1) % MT;
+        if constexpr ((v & 1) == 0)
+          dv[mt] = E::mfma(tf[v], __builtin_bit_cast(half8, pp[h2]), dv[mt]);
+        else
+          dk[mt] = E::mfma(tf[v], __builtin_bit_cast(half8, pd[h2]), dk[mt]);
+      }
+      static_for<4>([&](auto g_c) {
+        if constexpr (stats_slot(decltype(g_c)::value) == slot) read_stats(g_c);
+      });
+      static_for<8>([&](auto p_c) {
+        if constexpr (pair_slot(decltype(p_c)::value) == slot) softmax_pair(p_c);
+      });
+      fence_schedule();
+    });
+    if constexpr (HAS_NEXT) mask_scores(sb[TN], T == 0 ? s : s + 1, TN);
+  };
+
+  // Step s on stage B; LAST: no step s+1.
+  auto step = [&](int s, auto b_c, auto last_c) {
+    constexpr int B = decltype(b_c)::value;
+    constexpr bool LAST = decltype(last_c)::value;
+    phase(s, std::integral_constant<int, 0>{}, b_c, Flag<true>{});
+    // Step s+1's tiles have landed, and every wave is past its last read of
+    // stage B+2 (step s-1), which now receives step s+2.
+    barrier_after_loads<0>();
+    if (s + 2 < steps) issue(s + 2, std::integral_constant<int, B + 2>{});
+    phase(s, std::integral_constant<int, 1>{}, b_c, Flag<!LAST>{});
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  if (steps > 0) {
+    issue(0, I0{});
+    if (steps > 1) {
+      issue(1, I1{});
+      barrier_after_loads<2 * SEGQ>();  // step 0's loads (wave 0: and one of step 1's)
+    } else {
+      barrier_after_loads<0>();
+    }
+    // S and dP of sub-tile (0, 0).
+    sb[0] = db[0] = (float16v)0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      sb[0] = E::mfma(rd.row(q_lds0, 0, kk), kf[kk], sb[0]);
+      db[0] = E::mfma(rd.row(d_lds0, 0, kk), vf[kk], db[0]);
+    }
+    mask_scores(sb[0], 0, 0);
+    int s = 0;
+    for (; s + 3 < steps; s += 3) {
+      step(s, I0{}, Flag<false>{});
+      step(s + 1, I1{}, Flag<false>{});
+      step(s + 2, I2{}, Flag<false>{});
+    }
+    const int rest = steps - s;  // 1..3
+    if (rest == 1) {
+      step(s, I0{}, Flag<true>{});
+    } else if (rest == 2) {
+      step(s, I0{}, Flag<false>{});
+      step(s + 1, I1{}, Flag<true>{});
+    } else {
+      step(s, I0{}, Flag<false>{});
+      step(s + 1, I1{}, Flag<false>{});
+      step(s + 2, I2{}, Flag<true>{});
+    }
   }
-  if (s < steps) step(s, std::integral_constant<int, 0>{});
 
   if (krow < NK) {
     _Float16* dkp = a.dk + b * a.dksb + hkv * a.dksh + (int64_t)krow * a.dksn;
