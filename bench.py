@@ -260,7 +260,7 @@ def time_sdpa_decode_call(keys, n=200):
     return out
 
 
-def time_backward(cfg, steps=10, warmup=3):
+def time_backward(cfg, steps=10, warmup=3, dtype="fp16"):
     """Average time of one flash_attention_backward call (stats, dK/dV and dQ
     kernels) on the workload's shape, HIP events on the launch stream around
     the timed calls; inputs, O, LSE and dO resident in HBM."""
@@ -271,10 +271,11 @@ def time_backward(cfg, steps=10, warmup=3):
     B, Hq, Hkv, N, D, causal, std, _ = CONFIGS[cfg]
     dev = torch.device("cuda", 0)
     g = torch.Generator("cpu").manual_seed(11)
-    q = (torch.randn(B, Hq, N, D, generator=g) * std).half().to(dev)
-    k = (torch.randn(B, Hkv, N, D, generator=g) * std).half().to(dev)
-    v = (torch.randn(B, Hkv, N, D, generator=g) * std).half().to(dev)
-    do = torch.randn(B, Hq, N, D, generator=g).half().to(dev)
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    q = (torch.randn(B, Hq, N, D, generator=g) * std).to(dt).to(dev)
+    k = (torch.randn(B, Hkv, N, D, generator=g) * std).to(dt).to(dev)
+    v = (torch.randn(B, Hkv, N, D, generator=g) * std).to(dt).to(dev)
+    do = torch.randn(B, Hq, N, D, generator=g).to(dt).to(dev)
     o, lse = flash_attention_forward_ex(q, k, v, causal=causal, return_lse=True)
     for _ in range(warmup):
         flash_attention_backward(do, q, k, v, o, lse, causal=causal)
@@ -409,6 +410,11 @@ def main():
             med = km[len(km) // 2]
             log(f"[{c}] {DESCR[c]}: median kernel {med:.4f} ms -> "
                 f"{flops(b_, hq_, n_, d_, ca_) / med / 1e9:.1f} TFLOPS")
+            if not args.no_backward:
+                for dt in ("fp16", "bf16"):
+                    bms = time_backward(c, 5, 2, dt)
+                    log(f"[{c} backward {dt}] {bms:.4f} ms -> "
+                        f"{2.5 * flops(b_, hq_, n_, d_, ca_) / bms / 1e9:.1f} TFLOPS (2.5x fwd FLOPs)")
 
     if args.decode_only:  # profiling aid: one decode workload, nothing else
         ms, gbs = time_decode(args.decode_only, steps=args.steps, warmup=args.warmup)
