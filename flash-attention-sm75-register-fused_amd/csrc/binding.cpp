@@ -162,8 +162,9 @@ int64_t eff_stride(const torch::Tensor& t, int i, int64_t fallback) {
 // Packs a boolean mask broadcastable to [B, Hq, Nq, Nk] into bit rows; the
 // mask's own size-1 (or stride-0) batch, head and query dimensions stay size
 // 1 in the packed tensor and get stride 0 in the params.
+template <class Params>  // fa_fwd_params or fa_bwd_params (same mask fields)
 torch::Tensor pack_mask(const torch::Tensor& mask, const torch::Tensor& Q, int64_t nk,
-                        fa_fwd_params& p) {
+                        Params& p) {
   TORCH_CHECK(mask.dtype() == torch::kBool, "attn_mask must be a bool tensor");
   TORCH_CHECK(mask.device() == Q.device(), "attn_mask must be on Q's device");
   TORCH_CHECK(mask.dim() <= 4, "attn_mask must have at most 4 dimensions");
@@ -242,13 +243,14 @@ std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_
 
 // ---- flash_attention_backward: dQ, dK, dV (no reference counterpart) ---------
 
-// Gradients of flash_attention_forward_ex's O (causal code and scale as
-// given to it) from dO, the inputs, O and the fp32 row LSE it returned.
+// Gradients of flash_attention_forward_ex's O (causal code, scale and
+// boolean attn_mask as given to it) from dO, the inputs, O and the fp32 row
+// LSE it returned.
 // Inputs are read in place when their layout allows; the gradients are
 // dense tensors shaped like Q, K and V.
 std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_backward(
     torch::Tensor dO, torch::Tensor Q, torch::Tensor K, torch::Tensor V, torch::Tensor O,
-    torch::Tensor LSE, int64_t causal, double scale) {
+    torch::Tensor LSE, int64_t causal, double scale, c10::optional<torch::Tensor> attn_mask) {
   for (auto* pr : {&Q, &K, &V, &O, &dO}) {
     const torch::Tensor& t = *pr;
     TORCH_CHECK(t.is_cuda(), "inputs must be CUDA tensors");
@@ -320,6 +322,8 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_backward
   p.causal = (int)causal;
   p.dtype = Q.scalar_type() == torch::kBFloat16 ? FA_DTYPE_BF16 : FA_DTYPE_FP16;
   p.stream = c10::hip::getCurrentHIPStream(Q.device().index()).stream();
+  torch::Tensor bits;  // lives until the launches are enqueued (stream-ordered reuse)
+  if (attn_mask.has_value()) bits = pack_mask(*attn_mask, Q, K.size(2), p);
   const int64_t ws = fa_sm75_backward_workspace_size(&p);
   torch::Tensor work;  // released after the launch: stream-ordered reuse
   if (ws > 0) {
@@ -398,7 +402,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "fp32 row LSE; causal 0 none, 1 top-left, 2 bottom-right",
         pybind11::arg("dO"), pybind11::arg("Q"), pybind11::arg("K"), pybind11::arg("V"),
         pybind11::arg("O"), pybind11::arg("LSE"), pybind11::arg("causal"),
-        pybind11::arg("scale"));
+        pybind11::arg("scale"), pybind11::arg("attn_mask") = pybind11::none());
   m.def("abi_version", []() { return fa_sm75_abi_version(); });
   m.def("set_kernel_policy", [](int policy) {
     TORCH_CHECK(fa_sm75_set_kernel_policy(policy) == FA_OK,

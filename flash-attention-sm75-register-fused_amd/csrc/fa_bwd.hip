@@ -1,6 +1,6 @@
 // Fused attention backward for gfx950: grid plan and instance selection.
-// The kernels are in fa_bwd_kernel.h, instantiated per head dimension in
-// fa_bwd_d64.hip and fa_bwd_d128.hip.
+// The kernels are in fa_bwd_kernel.h, instantiated per head dimension and
+// mask mode in fa_bwd_d{64,128}{,_mask}.hip.
 #include <hip/hip_runtime.h>
 
 #include "fa_internal.h"
@@ -16,12 +16,24 @@ int launch_backward(const BwdArgs& args, int batch, int head_dim, bool causal, b
   a.num_qblocks = (a.n + kBwdBlockRows - 1) / kBwdBlockRows;
   a.items = batch * a.hq * a.num_qblocks;
   a.pair_half = 0;
+  a.mwords = (a.nk + 63) / 64;
+  const bool mask = a.mbits != nullptr;
   if (head_dim == 128) {
-    if (bf16) launch_bwd<128, true>(a, batch, causal, stream);
-    else launch_bwd<128, false>(a, batch, causal, stream);
+    if (mask) {
+      if (bf16) launch_bwd<128, true, true>(a, batch, causal, stream);
+      else launch_bwd<128, false, true>(a, batch, causal, stream);
+    } else {
+      if (bf16) launch_bwd<128, true, false>(a, batch, causal, stream);
+      else launch_bwd<128, false, false>(a, batch, causal, stream);
+    }
   } else {
-    if (bf16) launch_bwd<64, true>(a, batch, causal, stream);
-    else launch_bwd<64, false>(a, batch, causal, stream);
+    if (mask) {
+      if (bf16) launch_bwd<64, true, true>(a, batch, causal, stream);
+      else launch_bwd<64, false, true>(a, batch, causal, stream);
+    } else {
+      if (bf16) launch_bwd<64, true, false>(a, batch, causal, stream);
+      else launch_bwd<64, false, false>(a, batch, causal, stream);
+    }
   }
   return 0;
 }

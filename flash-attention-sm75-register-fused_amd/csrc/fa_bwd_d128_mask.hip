@@ -1,0 +1,7 @@
+// Backward instances: head_dim 128, explicit boolean mask, binary16 and bfloat16 (stats, dK/dV and dQ kernels).
+#include "fa_bwd_kernel.h"
+
+namespace fa {
+template void launch_bwd<128, false, true>(const BwdArgs&, int, bool, hipStream_t);
+template void launch_bwd<128, true, true>(const BwdArgs&, int, bool, hipStream_t);
+}  // namespace fa

@@ -2,6 +2,6 @@
 #include "fa_bwd_kernel.h"
 
 namespace fa {
-template void launch_bwd<64, false>(const BwdArgs&, int, bool, hipStream_t);
-template void launch_bwd<64, true>(const BwdArgs&, int, bool, hipStream_t);
+template void launch_bwd<64, false, false>(const BwdArgs&, int, bool, hipStream_t);
+template void launch_bwd<64, true, false>(const BwdArgs&, int, bool, hipStream_t);
 }  // namespace fa

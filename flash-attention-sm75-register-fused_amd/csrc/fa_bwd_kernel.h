@@ -158,7 +158,15 @@ __global__ void __launch_bounds__(256) fa_bwd_stats_kernel(const BwdArgs a) {
 // releases the buffer of step s-1, which then receives step s+2.
 typedef float float4v __attribute__((ext_vector_type(4)));
 
-template <int D, bool CAUSAL, bool BF16>
+// 4-byte direct load of one lane (lane l writes dst + 4 l).
+__device__ __forceinline__ void direct_load4(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 4, voff, 0, 0, 0);
+}
+
+// MASK: an explicit mask (fa_fwd_params bit rows) hides keys too; each
+// step also stages, per wave, the 32-bit word of every query row of the tile
+// that holds the wave's 32 keys (1 KB per stage).
+template <int D, bool CAUSAL, bool MASK, bool BF16>
 __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
   using L = Lds<D>;
   using E = Elem<BF16>;
@@ -179,6 +187,10 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
   __shared__ __attribute__((aligned(1024))) float s_lds0[256];
   __shared__ __attribute__((aligned(1024))) float s_lds1[256];
   __shared__ __attribute__((aligned(1024))) float s_lds2[256];
+  // MASK: word (wave w, row r) at w * 64 + r.
+  __shared__ __attribute__((aligned(1024))) uint32_t m_lds0[MASK ? 256 : 1];
+  __shared__ __attribute__((aligned(1024))) uint32_t m_lds1[MASK ? 256 : 1];
+  __shared__ __attribute__((aligned(1024))) uint32_t m_lds2[MASK ? 256 : 1];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = (int)threadIdx.x & 63;
@@ -246,6 +258,12 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
     else if constexpr (S == 1) return s_lds1;
     else return s_lds2;
   };
+  auto mbuf = [&](auto st) -> uint32_t* {
+    constexpr int S = decltype(st)::value % 3;
+    if constexpr (S == 0) return m_lds0;
+    else if constexpr (S == 1) return m_lds1;
+    else return m_lds2;
+  };
   auto qbase_of = [&](int s) {
     const int h = s / per_head;
     return (qt_begin + (s - h * per_head)) * kBwdStatsTile;
@@ -275,6 +293,16 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
           2 * kBwdStatsTile * 4);
       direct_load16(rs, (lds_void*)sbuf(st), 16 * lane);
     }
+    if constexpr (MASK) {
+      // Lane l: row q0 + l, 32-bit word 2 (k0 / 64) + wave of it; the window
+      // ends after the last row's words (rows past it and words past the
+      // keys read as 0).
+      const uint64_t* mrow = a.mbits + b * a.msb + hq * a.msh + (int64_t)q0 * a.msq;
+      const __amdgpu_buffer_rsrc_t rm =
+          make_rsrc(mrow, (int)((((int64_t)rows - 1) * a.msq + a.mwords) * 8));
+      direct_load4(rm, (lds_void*)(mbuf(st) + 64 * wave),
+                   (int)(lane * a.msq * 8) + (k0 / 64) * 8 + 4 * wave);
+    }
   };
 
   const TileReader<D> rd(lane);
@@ -282,9 +310,11 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
   // weights), so a score set to mval gives P = 0 exactly.
   const float c2 = a.c2 != 0.0f ? a.c2 : 1e-30f;
   const float mval = c2 > 0.0f ? -__builtin_inff() : __builtin_inff();
-  // Scores of sub-tile t of step s whose key is past the causal diagonal of
-  // their query (element i: query q0 + 8(i/4) + 4hi + i%4) -> mval.
-  auto mask_scores = [&](float16v& sv, int s, int t) {
+  // Scores of sub-tile t of step s (stage ST) whose key is past the causal
+  // diagonal of their query (element i: query q0 + 8(i/4) + 4hi + i%4) or
+  // hidden by the mask -> mval.
+  auto mask_scores = [&](float16v sv, int s, int t, auto st)
+                         __attribute__((always_inline)) -> float16v {
     if constexpr (CAUSAL) {
       const int q0 = qbase_of(s) + 32 * t;
       if (kw + 31 > q0 + a.diag) {
@@ -294,6 +324,18 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
         });
       }
     }
+    if constexpr (MASK) {
+      const uint32_t* mw = mbuf(st) + 64 * wave + 32 * t + 4 * hi;
+      static_for<4>([&](auto g_c) {
+        constexpr int g = decltype(g_c)::value;
+        const uint4v m4 = *(const uint4v*)(mw + 8 * g);
+        static_for<4>([&](auto e_c) {
+          constexpr int e = decltype(e_c)::value;
+          if (((m4[e] >> ql) & 1u) == 0) sv[4 * g + e] = mval;
+        });
+      });
+    }
+    return sv;
   };
 
   // S and dP of the current (index t) and next (1 - t) sub-tile.
@@ -395,7 +437,8 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
       });
       fence_schedule();
     });
-    if constexpr (HAS_NEXT) mask_scores(sb[TN], T == 0 ? s : s + 1, TN);
+    if constexpr (HAS_NEXT)
+      sb[TN] = mask_scores(sb[TN], T == 0 ? s : s + 1, TN, std::integral_constant<int, BN>{});
   };
 
   // Step s on stage B; LAST: no step s+1.
@@ -428,7 +471,7 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
       sb[0] = E::mfma(rd.row(q_lds0, 0, kk), kf[kk], sb[0]);
       db[0] = E::mfma(rd.row(d_lds0, 0, kk), vf[kk], db[0]);
     }
-    mask_scores(sb[0], 0, 0);
+    sb[0] = mask_scores(sb[0], 0, 0, I0{});
     int s = 0;
     for (; s + 3 < steps; s += 3) {
       step(s, I0{}, Flag<false>{});
@@ -474,8 +517,10 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
 // its block can see, K and V tiles double buffered through LDS.  Two
 // workgroups per CU (238 VGPRs, 80 KiB of LDS each): measured 26% faster
 // than one on the C4 training shape.
-template <int D, bool CAUSAL, bool BF16>
-__global__ void __launch_bounds__(256, 2) fa_bwd_dq_kernel(const BwdArgs a) {
+// Two workgroups per CU, except with a mask at head_dim 128 (its mask words
+// do not fit the 256 registers that allows).
+template <int D, bool CAUSAL, bool MASK, bool BF16>
+__global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kernel(const BwdArgs a) {
   using L = Lds<D>;
   using E = Elem<BF16>;
   constexpr int KK = D / 16;
@@ -521,6 +566,9 @@ __global__ void __launch_bounds__(256, 2) fa_bwd_dq_kernel(const BwdArgs a) {
 
   const int kv_len = CAUSAL ? max(0, min(NK, q0 + kBwdBlockRows + a.diag)) : NK;
   const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
+  // MASK: the lane's mask row (rows past N read row N - 1; not stored).
+  const uint64_t* mrow =
+      MASK ? a.mbits + b * a.msb + hq * a.msh + (int64_t)min(qrow, N - 1) * a.msq : nullptr;
 
   int goff_k[SEGQ], goff_v[SEGQ];
 #pragma unroll
@@ -552,7 +600,10 @@ __global__ void __launch_bounds__(256, 2) fa_bwd_dq_kernel(const BwdArgs a) {
     const _Float16* vc = PAR ? v_lds1 : v_lds0;
     if (j + 1 < ntiles) issue(j + 1, PAR ? k_lds0 : k_lds1, PAR ? v_lds0 : v_lds1);
     const int kstart = j * kBlockN;
-    const bool need_mask = kstart + kBlockN > NK || (CAUSAL && kstart + kBlockN - 1 > qw + a.diag);
+    // MASK: bit k of mw = key kstart + k visible to this lane's query.
+    const uint64_t mw = MASK ? mrow[j] : ~0ull;
+    bool need_mask = kstart + kBlockN > NK || (CAUSAL && kstart + kBlockN - 1 > qw + a.diag);
+    if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
     uint4v pd[4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -567,9 +618,11 @@ __global__ void __launch_bounds__(256, 2) fa_bwd_dq_kernel(const BwdArgs a) {
         float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i], c2, -lse2));
         float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i + 1], c2, -lse2));
         if (need_mask) {
-          const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
-          if (key >= NK || (CAUSAL && key > qrow + a.diag)) p0 = 0.0f;
-          if (key + 1 >= NK || (CAUSAL && key + 1 > qrow + a.diag)) p1 = 0.0f;
+          const int kt = 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);  // key within the tile
+          const int key = kstart + kt;
+          if (key >= NK || (CAUSAL && key > qrow + a.diag) || ((mw >> kt) & 1) == 0) p0 = 0.0f;
+          if (key + 1 >= NK || (CAUSAL && key + 1 > qrow + a.diag) || ((mw >> (kt + 1)) & 1) == 0)
+            p1 = 0.0f;
         }
         put_pair<E>(pd, t, i, p0 * (dpa[i] - delta), p1 * (dpa[i + 1] - delta));
       }
@@ -611,7 +664,7 @@ __global__ void __launch_bounds__(256, 2) fa_bwd_dq_kernel(const BwdArgs a) {
 
 // Launches the three backward kernels for head dimension D (the launcher in
 // fa_bwd.hip has planned the grids).
-template <int D, bool BF16>
+template <int D, bool BF16, bool MASK>
 void launch_bwd(const BwdArgs& a, int batch, bool causal, hipStream_t stream) {
   const int stats_wgs = batch * a.hq * a.qtiles;
   const int dkdv_wgs = a.units * ((a.nk + kBwdBlockKeys - 1) / kBwdBlockKeys);
@@ -620,17 +673,17 @@ void launch_bwd(const BwdArgs& a, int batch, bool causal, hipStream_t stream) {
     hipLaunchKernelGGL((fa_bwd_stats_kernel<D, BF16>), dim3(stats_wgs), dim3(256), 0, stream, a);
   if (causal) {
     if (dkdv_wgs > 0)
-      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, true, BF16>), dim3(dkdv_wgs), dim3(256), 0,
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, true, MASK, BF16>), dim3(dkdv_wgs), dim3(256), 0,
                          stream, a);
     if (dq_wgs > 0)
-      hipLaunchKernelGGL((fa_bwd_dq_kernel<D, true, BF16>), dim3(dq_wgs), dim3(256), 0, stream,
+      hipLaunchKernelGGL((fa_bwd_dq_kernel<D, true, MASK, BF16>), dim3(dq_wgs), dim3(256), 0, stream,
                          a);
   } else {
     if (dkdv_wgs > 0)
-      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, false, BF16>), dim3(dkdv_wgs), dim3(256), 0,
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, false, MASK, BF16>), dim3(dkdv_wgs), dim3(256), 0,
                          stream, a);
     if (dq_wgs > 0)
-      hipLaunchKernelGGL((fa_bwd_dq_kernel<D, false, BF16>), dim3(dq_wgs), dim3(256), 0, stream,
+      hipLaunchKernelGGL((fa_bwd_dq_kernel<D, false, MASK, BF16>), dim3(dq_wgs), dim3(256), 0, stream,
                          a);
   }
 }

@@ -282,6 +282,20 @@ int validate_bwd(const fa_bwd_params* p) {
   if (p->batch * p->heads_q * ((p->seq_len + 63) / 64) >= (int64_t)(1u << 24) ||
       p->batch * p->heads_kv * ((nk + 127) / 128) >= (int64_t)(1u << 24))
     return fail(FA_ERR_TOO_LARGE, "the backward grids exceed 2^24 workgroups");
+  if (p->mask_bits != nullptr) {
+    if ((reinterpret_cast<uintptr_t>(p->mask_bits) & 7u) != 0)
+      return fail(FA_ERR_MISALIGNED, "mask_bits must be 8-byte aligned");
+    if (p->mask_stride_b < 0 || p->mask_stride_h < 0 || p->mask_stride_q < 0)
+      return fail(FA_ERR_INVALID_ARGUMENT, "mask strides must be non-negative");
+    const int64_t words = (nk + 63) / 64;
+    if (p->mask_stride_q != 0 && p->mask_stride_q < words)
+      return fail(FA_ERR_INVALID_ARGUMENT,
+                  "mask row stride %lld is below ceil(seq_len_kv / 64) = %lld words",
+                  (long long)p->mask_stride_q, (long long)words);
+    // The dK/dV kernel reads a tile's mask words through a 32-bit buffer window.
+    if ((p->seq_len * p->mask_stride_q + words) * 8 > (int64_t)INT32_MAX)
+      return fail(FA_ERR_TOO_LARGE, "seq_len * mask row stride exceeds 2^31 bytes");
+  }
   const int64_t need = fa::bwd_workspace_bytes(p->batch, p->heads_q, p->seq_len);
   if (p->workspace_bytes < need)
     return fail(FA_ERR_INVALID_ARGUMENT, "workspace_bytes %lld is below the required %lld",
@@ -421,6 +435,10 @@ int fa_sm75_backward(const fa_bwd_params* p) {
   a.dksb = p->dk_stride_b; a.dksh = p->dk_stride_h; a.dksn = p->dk_stride_n;
   a.dvsb = p->dv_stride_b; a.dvsh = p->dv_stride_h; a.dvsn = p->dv_stride_n;
   a.stats = static_cast<float*>(p->workspace);
+  a.mbits = p->mask_bits;
+  a.msb = p->mask_stride_b;
+  a.msh = p->mask_stride_h;
+  a.msq = p->mask_stride_q;
   a.n = (int)p->seq_len;
   a.nk = (int)bwd_kv_rows(p);
   a.diag = p->causal == FA_CAUSAL_BOTTOM_RIGHT ? a.nk - a.n : 0;

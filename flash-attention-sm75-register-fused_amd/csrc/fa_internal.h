@@ -141,6 +141,9 @@ struct BwdArgs {
   // lse * log2(e) (+inf for rows past N and rows that see no key), then 64
   // floats rowsum(dO * O) (0 past N).
   float* stats;
+  const uint64_t* mbits;   // explicit mask bits (fa_fwd_params layout) or nullptr
+  int64_t msb, msh, msq;   // its strides in 64-bit words
+  int mwords;              // ceil(nk / 64): words of one mask row
   int n;       // query rows
   int nk;      // key/value rows
   int diag;    // causal: key j visible to query i iff j <= i + diag
@@ -167,7 +170,7 @@ inline int64_t bwd_workspace_bytes(int64_t batch, int64_t heads_q, int64_t seq_l
 // Launches the stats, dK/dV and dQ kernels; all arguments validated.
 int launch_backward(const BwdArgs& a, int batch, int head_dim, bool causal, bool bf16,
                     hipStream_t stream);
-template <int D, bool BF16>
+template <int D, bool BF16, bool MASK>
 void launch_bwd(const BwdArgs& a, int batch, bool causal, hipStream_t stream);
 
 // Boolean mask -> bit rows (fa_mask.hip).

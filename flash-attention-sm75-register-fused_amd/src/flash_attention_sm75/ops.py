@@ -170,25 +170,28 @@ class FlashAttentionFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, Q, K, V, code, scale):
-        O, LSE = _C.flash_attention_forward_ex(Q, K, V, code, scale, True, None)
+    def forward(ctx, Q, K, V, code, scale, attn_mask):
+        O, LSE = _C.flash_attention_forward_ex(Q, K, V, code, scale, True, attn_mask)
         ctx.save_for_backward(Q, K, V, O, LSE)
         ctx.code = code
         ctx.scale = scale
+        ctx.attn_mask = attn_mask
         return O
 
     @staticmethod
     def backward(ctx, dO):
         Q, K, V, O, LSE = ctx.saved_tensors
-        dQ, dK, dV = _C.flash_attention_backward(dO, Q, K, V, O, LSE, ctx.code, ctx.scale)
-        return dQ, dK, dV, None, None
+        dQ, dK, dV = _C.flash_attention_backward(dO, Q, K, V, O, LSE, ctx.code, ctx.scale,
+                                                 ctx.attn_mask)
+        return dQ, dK, dV, None, None, None
 
 
-def flash_attention(Q, K, V, causal=False, scale=None):
+def flash_attention(Q, K, V, causal=False, scale=None, attn_mask=None):
     """Fused attention with a backward pass (training).
 
     Same inputs as :func:`flash_attention_forward_ex` (fp16 or bf16, grouped
-    K/V heads, N_q != N_k, either causal alignment), no ``attn_mask``.  When
+    K/V heads, N_q != N_k, either causal alignment, a boolean ``attn_mask``,
+    which is not differentiated).  When
     autograd records the call, the backward computes dQ, dK and dV with the
     fused MFMA kernels (deterministic; for grouped heads dK and dV sum over
     each KV head's query heads).  No reference counterpart.
@@ -207,13 +210,14 @@ def flash_attention(Q, K, V, causal=False, scale=None):
         ) from None
     _check_gqa_heads(Q, K)
     if torch.is_grad_enabled() and (Q.requires_grad or K.requires_grad or V.requires_grad):
-        return FlashAttentionFunction.apply(Q, K, V, code, float(scale))
-    return _C.flash_attention_forward_ex(Q, K, V, code, float(scale), False, None)[0]
+        return FlashAttentionFunction.apply(Q, K, V, code, float(scale), attn_mask)
+    return _C.flash_attention_forward_ex(Q, K, V, code, float(scale), False, attn_mask)[0]
 
 
-def flash_attention_backward(dO, Q, K, V, O, LSE, causal=False, scale=None):
+def flash_attention_backward(dO, Q, K, V, O, LSE, causal=False, scale=None, attn_mask=None):
     """Gradients (dQ, dK, dV) of ``O = flash_attention_forward_ex(Q, K, V,
-    causal, scale)`` given dO and that call's LSE (``return_lse=True``).
+    causal, scale, attn_mask=attn_mask)`` given dO and that call's LSE
+    (``return_lse=True``).
 
     No reference counterpart.  Deterministic; fp16 or bf16 like the inputs.
     """
@@ -227,4 +231,4 @@ def flash_attention_backward(dO, Q, K, V, O, LSE, causal=False, scale=None):
             f"causal must be False, True, 'top_left' or 'bottom_right', got {causal!r}"
         ) from None
     _check_gqa_heads(Q, K)
-    return _C.flash_attention_backward(dO, Q, K, V, O, LSE, code, float(scale))
+    return _C.flash_attention_backward(dO, Q, K, V, O, LSE, code, float(scale), attn_mask)

@@ -21,8 +21,7 @@ without changing results:
   * bfloat16 calls (most current models' dtype) run on the kernel's bfloat16
     instances; other dtypes, and mixed ones, fall back;
   * calls that need gradients (training) run on :func:`flash_attention`,
-    whose backward is the fused dQ/dK/dV kernels; with a boolean mask they
-    fall back (the backward takes no mask).
+    whose backward is the fused dQ/dK/dV kernels (boolean masks included).
 """
 import torch
 import torch.nn.functional as F
@@ -72,8 +71,6 @@ def _fallback_reason(query, key, value, attn_mask, dropout_p, is_causal, kwargs)
         return "empty_kv"
     if set(kwargs) - {"enable_gqa"}:
         return "unsupported_kwargs"
-    if attn_mask is not None and _needs_grad(query, key, value):
-        return "requires_grad"  # the backward kernels take no mask
     return None
 
 
@@ -93,7 +90,8 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
                               is_causal=is_causal, scale=scale, **kwargs)
     _stats["flash"] += 1
     if _needs_grad(query, key, value):
-        return flash_attention(query, key, value, causal=bool(is_causal), scale=scale)
+        return flash_attention(query, key, value, causal=bool(is_causal), scale=scale,
+                               attn_mask=attn_mask)
     return flash_attention_forward_ex(query, key, value, causal=bool(is_causal), scale=scale,
                                       attn_mask=attn_mask)
 

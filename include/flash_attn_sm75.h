@@ -185,7 +185,7 @@ int fa_sm75_get_kernel_policy(void);
  * [B, Hkv, Nk, D] (for grouped heads each KV head's gradient sums over its
  * query heads).  P and dS are rounded to the element type before the
  * products that take them; sums are fp32.  Deterministic: the same inputs
- * give bitwise the same gradients.  No explicit mask. */
+ * give bitwise the same gradients. */
 typedef struct fa_bwd_params {
   const fa_half* q;     /* [B, Hq,  N,  D] */
   const fa_half* k;     /* [B, Hkv, Nk, D] */
@@ -219,6 +219,11 @@ typedef struct fa_bwd_params {
                            fa_sm75_backward_workspace_size() bytes, 16-byte
                            aligned (required); calls that share one race */
   int64_t workspace_bytes;
+  /* Optional explicit mask, or NULL: the forward's (fa_fwd_params.mask_bits,
+   * same bit layout and word strides, 0 broadcasts a dimension); combines
+   * (AND) with `causal`.  The LSE must come from a forward with this mask. */
+  const uint64_t* mask_bits;
+  int64_t mask_stride_b, mask_stride_h, mask_stride_q;
 } fa_bwd_params;
 
 /* Fills contiguous strides for every tensor of *p from its sizes. */

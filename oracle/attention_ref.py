@@ -208,7 +208,7 @@ def attention_f64(Q, K, V, causal=False, scale=None, attn_mask=None):
     return np.matmul(E / np.where(tot > 0, tot, 1.0), v)
 
 
-def attention_backward_f64(Q, K, V, dO, causal=False, scale=None):
+def attention_backward_f64(Q, K, V, dO, causal=False, scale=None, attn_mask=None):
     """Gradients (dQ, dK, dV) of attention_f64's O in float64, closed form.
 
     No reference counterpart: the reference's autograd backward raises
@@ -218,7 +218,9 @@ def attention_backward_f64(Q, K, V, dO, causal=False, scale=None):
       dS = P o (dP - rowsum(dP o P)), dQ = scale dS K, dK = scale dS^T Q.
     A KV head shared by a group of query heads gets the sum of the group's
     gradients (the adjoint of the repeat_interleave at ops.py:24-26).  Rows
-    that see no key have P = 0 and contribute nothing.
+    that see no key have P = 0 and contribute nothing.  ``attn_mask``: a
+    boolean mask (True = visible) broadcastable to [B, Hq, Nq, Nk], as in
+    :func:`attention_reference`.
     """
     Q = np.asarray(Q)
     K = np.asarray(K)
@@ -236,6 +238,9 @@ def attention_backward_f64(Q, K, V, dO, causal=False, scale=None):
     mask = causal_mask(N, Nk, causal)
     if mask is not None:
         S[..., mask] = -np.inf
+    vis = visible(attn_mask, S.shape)
+    if vis is not None:
+        S[~vis] = -np.inf
     m = S.max(axis=-1, keepdims=True)
     m = np.where(np.isfinite(m), m, 0.0)
     E = np.exp(S - m)

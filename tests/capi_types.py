@@ -46,4 +46,6 @@ class BwdParams(ctypes.Structure):
         ("scale", ctypes.c_float), ("causal", ctypes.c_int), ("dtype", ctypes.c_int),
         ("stream", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_int64),
+        ("mask_bits", ctypes.c_void_p), ("mask_stride_b", ctypes.c_int64),
+        ("mask_stride_h", ctypes.c_int64), ("mask_stride_q", ctypes.c_int64),
     ]

@@ -74,6 +74,10 @@ def test_workspace_size(lib):
     (dict(workspace_bytes=100), 1, b"below the required"),
     (dict(seq_len_kv=1 << 30), 5, b"exceeds the supported maximum"),
     (dict(q_stride_n=1 << 24), 5, b"exceeds 2^31 bytes"),
+    (dict(mask_bits=0x10004), 4, b"mask_bits must be 8-byte aligned"),
+    (dict(mask_bits=0x10000, mask_stride_h=-1), 1, b"mask strides must be non-negative"),
+    (dict(mask_bits=0x10000, mask_stride_q=1), 1, b"mask row stride 1 is below"),
+    (dict(mask_bits=0x10000, mask_stride_q=1 << 22), 5, b"mask row stride exceeds 2^31"),
 ])
 def test_validation_errors(lib, kw, status, msg):
     p = make(lib, **kw)

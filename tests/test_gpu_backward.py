@@ -225,3 +225,33 @@ def test_graph_capture_replays(device):
         assert torch.isfinite(junk)
         for x, y in zip(outs, expect):
             assert torch.equal(x, y), rep
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,Hq,Hkv,Nq,Nk,D,causal,mshape", [
+    (2, 4, 2, 200, 200, 128, False, "b1qk"),
+    (1, 4, 4, 150, 300, 64, True, "bhqk"),
+    (2, 8, 2, 333, 333, 128, "bottom_right", "qk"),
+    (1, 2, 1, 257, 129, 64, False, "b1qk"),
+])
+def test_backward_with_mask(device, dtype, B, Hq, Hkv, Nq, Nk, D, causal, mshape):
+    """Boolean attn_mask (broadcast over batch/heads/rows as given), combined
+    with the causal modes, including rows that see no key; through the
+    autograd Function."""
+    print(f"[bwd mask] {dtype} B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} "
+          f"causal={causal} mask={mshape}", flush=True)
+    shape = {"b1qk": (B, 1, Nq, Nk), "bhqk": (B, Hq, Nq, Nk), "qk": (Nq, Nk)}[mshape]
+    g = torch.Generator("cpu").manual_seed(50)
+    mask = torch.rand(*shape, generator=g) < 0.7
+    mask[..., 5, :] = False  # a row that sees no key
+    q, k, v = seeded((B, Hq, Nq, D), 51, dtype), seeded((B, Hkv, Nk, D), 52, dtype), \
+        seeded((B, Hkv, Nk, D), 53, dtype)
+    do = seeded((B, Hq, Nq, D), 54, dtype)
+    leaves = [t.to(device).requires_grad_() for t in (q, k, v)]
+    o = flash_attention(*leaves, causal=causal, attn_mask=mask.to(device))
+    o.backward(do.to(device))
+    torch.cuda.synchronize()
+    want = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=CODE[causal],
+                                      attn_mask=mask.numpy())
+    assert torch.count_nonzero(leaves[0].grad[:, :, 5]) == 0
+    assert_grads([l.grad for l in leaves], want, dtype, f"mask {mshape}")

@@ -161,12 +161,8 @@ def test_patched_sdpa_fallbacks(device, patched):
         got = F.scaled_dot_product_attention(a, b, c, **kw)
         want = sp._original_sdpa(a, b, c, **kw)
         assert torch.equal(got, want), reason
-    qg = q.clone().requires_grad_(True)
-    F.scaled_dot_product_attention(qg, q, q, attn_mask=torch.ones(16, 16, dtype=torch.bool,
-                                                                   device=device))
-    torch.cuda.synchronize()
     reasons = sp._stats["fallback_reasons"]
-    for r in ("not_fp16", "head_dim_unsupported", "has_attn_mask", "requires_grad"):
+    for r in ("not_fp16", "head_dim_unsupported", "has_attn_mask"):
         assert reasons.get(r) == 1, (r, reasons)
     assert sp._stats["flash"] == 0
 

@@ -22,7 +22,7 @@ def rnd(shape, seed):
     return np.random.default_rng(seed).standard_normal(shape).astype(np.float16)
 
 
-def torch_grads(q, k, v, do, causal, scale):
+def torch_grads(q, k, v, do, causal, scale, attn_mask=None):
     """float64 autograd through torch's ops, GQA by repeat_interleave."""
     Q = torch.tensor(q.astype(np.float64), requires_grad=True)
     K = torch.tensor(k.astype(np.float64), requires_grad=True)
@@ -33,6 +33,8 @@ def torch_grads(q, k, v, do, causal, scale):
     mask = ref.causal_mask(q.shape[2], k.shape[2], causal)
     if mask is not None:
         S = S.masked_fill(torch.tensor(mask), float("-inf"))
+    if attn_mask is not None:
+        S = S.masked_fill(~torch.tensor(attn_mask), float("-inf"))
     P = torch.softmax(S, -1).nan_to_num(0.0)
     O = P @ Ve
     O.backward(torch.tensor(do.astype(np.float64)))
@@ -158,3 +160,19 @@ def test_planted_mistakes_are_detected(kind):
     # and the unplanted oracle passes the same checks
     good = ref.attention_backward_f64(q, k, v, do, causal=1)
     assert all(np.allclose(b, w, rtol=1e-9, atol=1e-11) for b, w in zip(good, want))
+
+
+@pytest.mark.parametrize("mshape,causal", [((2, 1, 9, 14), 0), ((1, 4, 9, 14), 1),
+                                           ((9, 14), 2), ((2, 4, 1, 14), 0)])
+def test_masked_matches_torch_autograd(mshape, causal):
+    """Boolean masks (broadcast shapes, combined with each causal mode, rows
+    that see no key) against autograd with the same masked_fill."""
+    q, k, v = rnd((2, 4, 9, 64), 31), rnd((2, 2, 14, 64), 32), rnd((2, 2, 14, 64), 33)
+    do = rnd((2, 4, 9, 64), 34)
+    mask = np.random.default_rng(35).random(mshape) < 0.6
+    if len(mshape) == 4 and mshape[2] > 1:
+        mask[..., 3, :] = False  # a row that sees no key
+    got = ref.attention_backward_f64(q, k, v, do, causal=causal, attn_mask=mask)
+    want = torch_grads(q, k, v, do, causal, ref.default_scale(64), attn_mask=mask)
+    for name, g, w in zip(("dQ", "dK", "dV"), got, want):
+        np.testing.assert_allclose(g, w, rtol=1e-9, atol=1e-11, err_msg=name)
