@@ -1,5 +1,5 @@
 // Fused attention backward kernels for gfx950 (MI355X / CDNA4), included by
-// the instance files fa_bwd_d64.hip and fa_bwd_d128.hip.
+// the instance files fa_bwd_d{64,128}{,_mask}.hip.
 //
 // Gradients of O = softmax(scale * Q K^T + mask) V, given dO = dL/dO, the
 // forward's O and its row log-sum-exp (no reference counterpart: the
@@ -16,11 +16,15 @@
 //     into the workspace in 64-row records (one direct load per tile).
 //   * fa_bwd_dkdv_kernel: one workgroup per (batch, KV head, 128 keys), wave
 //     w owning keys k0 + 32w .. +32 with their K and V rows resident in
-//     registers.  It streams 64-row tiles of Q and dO (and their stats)
-//     through LDS for every query head of the group, so the GQA sum over
-//     the group happens in the accumulators.
+//     registers.  It streams 64-row tiles of Q and dO (and their stats and
+//     mask words) through triple-buffered LDS for every query head of the
+//     group, so the GQA sum over the group happens in the accumulators;
+//     hand-ordered software pipeline, one workgroup per CU.
 //   * fa_bwd_dq_kernel: one workgroup per (batch, query head, 128 rows), the
-//     forward's shape: Q and dO rows resident, K and V tiles streamed.
+//     forward's shape: Q and dO rows resident, K and V tiles streamed through
+//     double-buffered LDS; two workgroups per CU.
+// An explicit boolean mask (MASK instances) hides keys on top of the causal
+// rule; rows that see no key have lse = -inf, so their P is 0.
 // Tiles use the forward's LDS layout (Lds<D>: padded rows, 16-byte chunks
 // XOR-swizzled), on which both operand reads below are conflict-free.
 //
