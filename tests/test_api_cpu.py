@@ -85,3 +85,35 @@ def test_product_path_has_no_oracle_import():
     assert not any(name == "oracle" or name.startswith("oracle.") for name in
                    getattr(m, "__dict__", {}))
     del sys
+
+
+def test_training_surface():
+    """The added differentiable entry points (no reference counterpart)."""
+    for name in ("flash_attention", "flash_attention_backward"):
+        assert name in fa.__all__ and callable(getattr(fa, name))
+    assert hasattr(_C, "flash_attention_backward")
+
+
+def test_flash_attention_argument_checks():
+    from flash_attention_sm75 import flash_attention, flash_attention_backward
+
+    with pytest.raises(ValueError, match=r"Q must be 4D"):
+        flash_attention(h(8, 128, 64), h(8, 128, 64), h(8, 128, 64))
+    with pytest.raises(RuntimeError, match="supports head_dim=64 or 128"):
+        flash_attention(h(1, 2, 8, 96), h(1, 2, 8, 96), h(1, 2, 8, 96))
+    with pytest.raises(ValueError, match="causal must be"):
+        flash_attention(h(1, 2, 8, 64), h(1, 2, 8, 64), h(1, 2, 8, 64), causal="diagonal")
+    with pytest.raises(RuntimeError, match=r"GQA expansion: Q heads \(6\)"):
+        flash_attention(h(1, 6, 8, 64), h(1, 4, 8, 64), h(1, 4, 8, 64))
+    q = h(1, 2, 8, 64)
+    lse = torch.zeros(1, 2, 8)
+    with pytest.raises(RuntimeError, match="inputs must be CUDA tensors"):
+        flash_attention_backward(q, q, q, q, q, lse)
+
+
+def test_backward_binding_checks_before_device():
+    q = h(1, 2, 8, 64)
+    with pytest.raises(RuntimeError, match="inputs must be CUDA tensors"):
+        _C.flash_attention_backward(q, q, q, q, q, torch.zeros(1, 2, 8), 0, 0.125)
+    with pytest.raises(TypeError):
+        _C.flash_attention_backward(q, q, q, q, q, torch.zeros(1, 2, 8))  # causal, scale required
