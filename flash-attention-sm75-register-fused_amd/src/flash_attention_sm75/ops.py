@@ -179,7 +179,10 @@ class FlashAttentionFunction(torch.autograd.Function):
         return O
 
     @staticmethod
+    @torch.autograd.function.once_differentiable
     def backward(ctx, dO):
+        # The backward kernels are not differentiable themselves: a double
+        # backward raises instead of returning wrong second derivatives.
         Q, K, V, O, LSE = ctx.saved_tensors
         dQ, dK, dV = _C.flash_attention_backward(dO, Q, K, V, O, LSE, ctx.code, ctx.scale,
                                                  ctx.attn_mask)

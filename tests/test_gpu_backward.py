@@ -130,6 +130,12 @@ def test_autograd_function(device):
         assert torch.equal(leaf.grad, d)
     want = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=1)
     assert_grads([l.grad for l in leaves], want, torch.float16, "autograd")
+    # no double backward through the kernels
+    leaves2 = [t.to(device).requires_grad_() for t in (q, k, v)]
+    gq, = torch.autograd.grad(flash_attention(*leaves2, causal=True).float().square().sum(),
+                              leaves2[0], create_graph=True)
+    with pytest.raises(RuntimeError):
+        gq.sum().backward()
     # the reference's Function still raises in backward (reference tests/test_api.py:38)
     x = [t.to(device).requires_grad_() for t in (q, k, v)]
     with pytest.raises(NotImplementedError, match="Backward pass is not implemented"):
