@@ -264,3 +264,26 @@ def test_backward_with_mask(device, dtype, B, Hq, Hkv, Nq, Nk, D, causal, mshape
                                       attn_mask=mask.numpy())
     assert torch.count_nonzero(leaves[0].grad[:, :, 5]) == 0
     assert_grads([l.grad for l in leaves], want, dtype, f"mask {mshape}")
+
+
+def test_side_stream(device):
+    """The backward runs on the caller's current stream (its workspace comes
+    from that stream's pool): a call on a side stream, with the default
+    stream busy, gives bitwise the same gradients."""
+    print("[bwd side stream]", flush=True)
+    B, Hq, Hkv, N, D = 2, 8, 2, 500, 128
+    q, k, v = seeded((B, Hq, N, D), 60), seeded((B, Hkv, N, D), 61), seeded((B, Hkv, N, D), 62)
+    do = seeded((B, Hq, N, D), 63)
+    want = run_backward(q, k, v, do, True, device)
+    qd, kd, vd, dod = (t.to(device) for t in (q, k, v, do))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device)
+    busy = torch.randn(4096, 4096, device=device)
+    with torch.cuda.stream(side):
+        o, lse = flash_attention_forward_ex(qd, kd, vd, causal=True, return_lse=True)
+        got = flash_attention_backward(dod, qd, kd, vd, o, lse, causal=True)
+    for _ in range(4):
+        busy = busy @ busy * 1e-3  # default-stream work meanwhile
+    torch.cuda.synchronize()
+    for x, y in zip(want, got):
+        assert torch.equal(x, y)
