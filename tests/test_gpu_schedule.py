@@ -55,15 +55,18 @@ def run(lib, q, k, v, causal, workspace=None, mask=None, stream=None):
     schedule runs (policy NARROW)."""
     B, Hq, N, D = q.shape
     Hkv, Nk = k.shape[1], k.shape[2]
-    o = torch.full_like(q, float("nan"))
-    lse = torch.full((B, Hq, N), float("nan"), dtype=torch.float32, device=q.device)
+    s = stream if stream is not None else torch.cuda.current_stream()
+    # The NaN fills run on the launch stream, so they are ordered before the
+    # kernel that overwrites them.
+    with torch.cuda.stream(s):
+        o = torch.full_like(q, float("nan"))
+        lse = torch.full((B, Hq, N), float("nan"), dtype=torch.float32, device=q.device)
     p = Params()
     p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr()
     p.batch, p.heads_q, p.heads_kv, p.seq_len, p.head_dim = B, Hq, Hkv, N, D
     p.seq_len_kv = Nk
     lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
     p.scale, p.causal = 1.0 / math.sqrt(D), causal
-    s = stream if stream is not None else torch.cuda.current_stream()
     p.stream = s.cuda_stream
     if workspace is not None:
         p.workspace, p.workspace_bytes = workspace.data_ptr(), workspace.numel()
