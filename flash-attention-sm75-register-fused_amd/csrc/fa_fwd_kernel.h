@@ -482,6 +482,11 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       static_for<16>([&](auto p_c) {
         if constexpr (pair_slot(decltype(p_c)::value) < 0) softmax_pair(p_c);
       });
+      // Head_dim 128: the wave issuing its MFMA slots outranks the other
+      // workgroup's wave on the SIMD while that one runs prepare / waits at its
+      // barrier (measured +1% on C4, +0.3% on C5; at head_dim 64, whose steps
+      // are VALU-bound, -2%, so not there).
+      if constexpr (D == 128) __builtin_amdgcn_s_setprio(1);
       static_for<(PFK < ns ? PFK : ns)>([&](auto i_c) {
         kf[decltype(i_c)::value] = read_k(Kn, decltype(i_c)::value);
       });
@@ -525,6 +530,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         fence_schedule();
       });
 
+      if constexpr (D == 128) __builtin_amdgcn_s_setprio(0);
       if (HAS_NEXT) {
         prepare(j + 1, s_nxt, mx_next, mw_next);
         // The loads of the previous step have landed (those of this step may
