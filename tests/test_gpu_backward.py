@@ -197,22 +197,29 @@ def test_empty_and_degenerate(device):
     assert all(t.numel() == 0 for t in out)
 
 
-def test_graph_capture_replays(device):
+@pytest.mark.parametrize("masked", [False, True])
+def test_graph_capture_replays(device, masked):
     """The backward captured in a HIP graph (three kernel launches, workspace
-    from the graph's pool, no memsets) and replayed three times with fresh
-    inputs and eager work in between: every replay bitwise equal to eager."""
-    print("[bwd graph]", flush=True)
+    from the graph's pool, no memsets; with a mask also the packing kernel
+    and the masked forward) and replayed three times with fresh inputs and
+    eager work in between: every replay bitwise equal to eager."""
+    print(f"[bwd graph] masked={masked}", flush=True)
     B, Hq, Hkv, N, D = 1, 8, 2, 700, 128
     q, k, v, do = (torch.empty(s, dtype=torch.float16, device=device)
                    for s in ((B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D), (B, Hq, N, D)))
+    mask = None
+    if masked:
+        g = torch.Generator("cpu").manual_seed(70)
+        mask = (torch.rand(B, 1, N, N, generator=g) < 0.8).to(device)
 
     def fill(seed):
         for i, t in enumerate((q, k, v, do)):
             t.copy_(seeded(t.shape, seed + i))
 
     def call():
-        o, lse = flash_attention_forward_ex(q, k, v, causal=True, return_lse=True)
-        return flash_attention_backward(do, q, k, v, o, lse, causal=True)
+        o, lse = flash_attention_forward_ex(q, k, v, causal=True, return_lse=True,
+                                            attn_mask=mask)
+        return flash_attention_backward(do, q, k, v, o, lse, causal=True, attn_mask=mask)
 
     fill(30)
     side = torch.cuda.Stream(device)
