@@ -300,7 +300,9 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
     if constexpr (MASK) {
       // Lane l: row q0 + l, 32-bit word 2 (k0 / 64) + wave of it; the window
       // ends after the last row's words (rows past it and words past the
-      // keys read as 0).
+      // keys read as 0).  Offsets of rows below N fit 32 bits (the C ABI
+      // checks N * row stride); a lane past N whose offset wraps reads 0 or
+      // some mask word inside the window, for a row that is never used.
       const uint64_t* mrow = a.mbits + b * a.msb + hq * a.msh + (int64_t)q0 * a.msq;
       const __amdgpu_buffer_rsrc_t rm =
           make_rsrc(mrow, (int)((((int64_t)rows - 1) * a.msq + a.mwords) * 8));
