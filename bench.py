@@ -2,7 +2,7 @@
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
                   [--no-cpu-baseline] [--no-gemm-ceiling] [--all] [--decode] [--hf]
-                  [--shape B,Hq,Hkv,N,D,causal] [--no-backward]
+                  [--shape B,Hq,Hkv,N,D,causal] [--no-backward] [--no-configs]
 
 A step is one fused forward over one batch of synthetic input (the hot path:
 flash_attention_sm75.flash_attention_forward -> flash_attn_sm75_cuda ->
@@ -25,6 +25,10 @@ Printed: ONE JSON line on stdout (rank 0).  Besides the driver's keys it holds
                 under the board's power limit, and the kernel's share of it;
   cpu_baseline  the reference math path (restated with torch on the host
                 CPU) timed on a bounded sample of the same workload;
+  configs       every BASELINE configuration C1-C5 (full and causal, head_dim
+                64 and 128), K launches each after W warm-up launches: kernel
+                average, median and min (HIP events on the launch stream),
+                TFLOPS and fraction of the MFMA peak;
   backward      the backward pass (dQ, dK, dV) on the same workload: its
                 average time and TFLOPS at 2.5x the forward's FLOP count.
 Diagnostics go to stderr.
@@ -127,6 +131,27 @@ def time_gpu(cfg, steps, warmup, data="randn"):
     return wall, kern_ms
 
 
+def kernel_stats(cfg, kern_ms):
+    """Per-launch statistics of one BASELINE configuration, in the form the
+    reference's benchmark reports them (median and min of HIP-event times,
+    reference benchmarks/benchmark_attention.py:150-171) plus the average."""
+    B, Hq, Hkv, N, D, causal, _, _ = CONFIGS[cfg]
+    F = flops(B, Hq, N, D, causal)
+    avg = sum(kern_ms) / len(kern_ms)
+    med = kern_ms[len(kern_ms) // 2]
+    return {
+        "workload": DESCR[cfg],
+        "kernel_avg_ms": round(avg, 5),
+        "kernel_median_ms": round(med, 5),
+        "kernel_min_ms": round(kern_ms[0], 5),
+        "tflops": round(F / (avg * 1e-3) / 1e12, 2),
+        "tflops_median": round(F / (med * 1e-3) / 1e12, 2),
+        "frac": round(F / (avg * 1e-3) / 1e12 / PEAK_TFLOPS, 4),
+        "flop": F,
+        "launches": len(kern_ms),
+    }
+
+
 def gemm_ceiling(m=16384, steps=5, warmup=2):
     """Dense fp16 GEMM (torch.matmul -> hipBLASLt) on N(0,1) data, m^3, timed
     with HIP events on the same GPU in the same run: what the MFMA pipes
@@ -156,17 +181,55 @@ def gemm_ceiling(m=16384, steps=5, warmup=2):
     return 2.0 * m ** 3 / (ms * 1e-3) / 1e12
 
 
+def host_cpu():
+    """The host's CPU model and counts: logical CPUs in the machine, the ones
+    this process may run on (its affinity mask), and the thread budget the
+    job is given (OMP_NUM_THREADS when the environment sets it)."""
+    import subprocess
+
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        m = re.search(r"^Model name:\s*(.+)$", out, re.M)
+        model = m.group(1).strip() if m else None
+        sockets = re.search(r"^Socket\(s\):\s*(\d+)$", out, re.M)
+        per_socket = re.search(r"^Core\(s\) per socket:\s*(\d+)$", out, re.M)
+        phys = (int(sockets.group(1)) * int(per_socket.group(1))
+                if sockets and per_socket else None)
+    except (OSError, ValueError, subprocess.SubprocessError):
+        phys = None
+    if model is None and os.path.exists("/proc/cpuinfo"):
+        m = re.search(r"^model name\s*:\s*(.+)$", open("/proc/cpuinfo").read(), re.M)
+        model = m.group(1).strip() if m else "unknown"
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    budget = int(omp) if omp.isdigit() and int(omp) > 0 else None
+    return {"model": model or "unknown", "logical_cpus": os.cpu_count() or 1,
+            "physical_cores": phys, "affinity_cpus": allowed, "omp_num_threads": budget}
+
+
 def cpu_baseline(cfg, budget_s=20.0, min_s=10.0):
     """Reference math path (torch on the host CPU) on a bounded sample: whole
     (batch, query-head) slices of the workload in order, stopping at
     ``budget_s``, or once every slice ran and at least ``min_s`` passed (the
-    slices are then repeated, so a fast host still times ~10 s of work)."""
+    slices are then repeated, so a fast host still times ~10 s of work).
+
+    Threads: every CPU this process may run on (its affinity mask), capped by
+    OMP_NUM_THREADS when the environment sets one -- a GPU box gives one
+    GPU's job a share of its host (16 CPUs per GPU) and says so there, so
+    more threads would only time contention with other jobs."""
     import torch
 
     from oracle import attention_ref as ref
 
     B, Hq, Hkv, N, D, causal, _, _ = CONFIGS[cfg]
-    threads = min(16, os.cpu_count() or 1)
+    host = host_cpu()
+    threads = host["affinity_cpus"]
+    if host["omp_num_threads"]:
+        threads = min(threads, host["omp_num_threads"])
     torch.set_num_threads(threads)
     q, k, v = make_inputs(cfg)
     done, t_used = 0, 0.0
@@ -183,6 +246,9 @@ def cpu_baseline(cfg, budget_s=20.0, min_s=10.0):
         "value": f / t_used / 1e12,
         "unit": "TFLOPS",
         "cores": threads,
+        "threads_rule": ("all CPUs in the process's affinity mask, capped by OMP_NUM_THREADS "
+                         "(the job's CPU share on the GPU box)"),
+        "host": host,
         "kind": "port",
         "sample": (f"{done} (batch, query-head) slices of {cfg} ({total} per workload, "
                    f"{done / total:.2f} workloads), all {N} rows each, {t_used:.1f} s; torch CPU "
@@ -365,6 +431,8 @@ def main():
                          "(the kernel is power-limited: less data toggling, higher clock)")
     ap.add_argument("--policy", type=int, default=0, choices=(0, 1, 2),
                     help="kernel policy: 0 auto, 1 = 128-row (4-wave), 2 = 256-row (8-wave)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip timing the other BASELINE configurations (C1-C5)")
     ap.add_argument("--no-backward", action="store_true",
                     help="skip timing the backward pass on the same workload")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -449,6 +517,21 @@ def main():
         f"(median {kern_ms[len(kern_ms) // 2]:.4f}, min {kern_ms[0]:.4f}) -> "
         f"{value:.1f} TFLOPS wall, {achieved:.1f} TFLOPS kernel")
 
+    # Every BASELINE configuration (the metric is "full + causal, d64/d128"):
+    # the same HIP-event timing per launch, reported beside the headline one.
+    per_config = {}
+    if cfg in CONFIGS and args.data == "randn" and not args.no_configs:
+        for c in sorted(k for k in CONFIGS if k.startswith("C")):
+            if c == cfg:
+                per_config[c] = kernel_stats(c, kern_ms)
+                continue
+            _, km = time_gpu(c, args.steps, args.warmup)
+            per_config[c] = kernel_stats(c, km)
+            log(f"[{c}] {DESCR[c]}: kernel avg {per_config[c]['kernel_avg_ms']:.4f} ms "
+                f"(median {per_config[c]['kernel_median_ms']:.4f}, min "
+                f"{per_config[c]['kernel_min_ms']:.4f}) -> {per_config[c]['tflops']:.1f} TFLOPS "
+                f"({100 * per_config[c]['frac']:.1f}% of peak)")
+
     ceiling = None
     if not args.no_gemm_ceiling:
         gemm = gemm_ceiling()
@@ -509,6 +592,7 @@ def main():
             "kernel_avg_ms": round(avg_kernel_ms, 5),
             "sustained_mfma": ceiling,
         },
+        "configs": per_config or None,
         "cpu_baseline": cpu,
         "backward": backward,
     }

@@ -145,7 +145,11 @@ bool kernel_layout_ok(const torch::Tensor& t, bool kv) {
   for (int i = 0; i < 3; ++i)
     if (t.size(i) > 1 && (t.stride(i) < 0 || t.stride(i) % 8 != 0)) return false;
   if (t.size(2) > 1 && t.stride(2) < t.size(3)) return false;
-  if (kv && t.size(2) * (t.size(2) > 1 ? t.stride(2) : t.size(3)) * 2 > (int64_t)INT32_MAX)
+  // The library reads these through 32-bit buffer windows that reach one
+  // 64-row tile past the last row (fa_capi.hip rejects (rows + 64) * row
+  // stride * 2 > INT32_MAX); such views are copied to a contiguous layout.
+  if (kv && (t.size(2) + 64) * (t.size(2) > 1 ? t.stride(2) : t.size(3)) * 2 >
+                (int64_t)INT32_MAX)
     return false;
   return true;
 }

@@ -472,7 +472,20 @@ void launch_decode_typed(const DecArgs& d, const DecodePlan& pl, int head_dim, b
 
 }  // namespace
 
-bool decode_eligible(const FwdArgs& a) { return (int64_t)a.group * a.n <= kDecodeMaxRows; }
+bool decode_eligible(const FwdArgs& a) {
+  if ((int64_t)a.group * a.n > kDecodeMaxRows) return false;
+  if (a.mbits != nullptr) {
+    // The split-K kernel reads one batch's mask rows through a single 32-bit
+    // buffer window (byte offsets up to this span); a call whose mask strides
+    // span more runs on the prefill kernel, which reads the words through
+    // 64-bit addresses.
+    const int64_t words = ((int64_t)a.nk + 63) / 64;
+    const int64_t span =
+        ((int64_t)(a.hq - 1) * a.msh + (int64_t)(a.n - 1) * a.msq + words) * 8;
+    if (span > (int64_t)INT32_MAX) return false;
+  }
+  return true;
+}
 
 DecodePlan plan_decode(const FwdArgs& a, int batch, int head_dim, bool causal,
                        int64_t workspace_bytes) {

@@ -17,7 +17,9 @@ without changing results:
   * Q/K/V views are read in place (transformers passes [B, N, H, D] buffers
     viewed as [B, H, N, D]) and O keeps Q's layout, so the caller's
     ``transpose(1, 2).contiguous()`` is free;
-  * grouped K/V heads go to the kernel as they are (no repeat_interleave);
+  * grouped K/V heads go to the kernel as they are (no repeat_interleave)
+    when the call says ``enable_gqa=True``; without it torch's SDPA rejects
+    grouped heads, so such calls pass through to torch and raise there;
   * bfloat16 calls (most current models' dtype) run on the kernel's bfloat16
     instances; other dtypes, and mixed ones, fall back;
   * calls that need gradients (training) run on :func:`flash_attention`,
@@ -67,6 +69,8 @@ def _fallback_reason(query, key, value, attn_mask, dropout_p, is_causal, kwargs)
         return "batch_mismatch"
     if key.size(1) == 0 or query.size(1) % key.size(1) != 0:
         return "heads_not_divisible"
+    if query.size(1) != key.size(1) and not kwargs.get("enable_gqa", False):
+        return "gqa_not_enabled"  # torch raises for grouped heads without enable_gqa
     if key.size(2) == 0:
         return "empty_kv"
     if set(kwargs) - {"enable_gqa"}:

@@ -114,7 +114,10 @@ def attention_reference_chunked(Q, K, V, causal=False, scale=None, rows=512,
 
     Rows of the softmax are independent, so evaluating [rows, N] blocks of S
     gives the same values as the full [N, N] matrix (up to fp32 summation
-    order inside BLAS).  ``heads`` restricts the computation to a list of
+    order inside BLAS).  Under a causal mask a row block only evaluates the
+    keys up to its last row's diagonal: the keys past it are hidden from
+    every row of the block, so they would contribute exp(-inf) = 0 to the
+    row sums and to P V.  ``heads`` restricts the computation to a list of
     query-head indices (output has only those heads), which the CPU baseline
     uses to time a bounded sample.
     """
@@ -139,17 +142,23 @@ def attention_reference_chunked(Q, K, V, causal=False, scale=None, rows=512,
             kf = K[b, h // group].astype(np.float32)
             vf = V[b, h // group].astype(np.float32)
             kt = np.ascontiguousarray(kf.T)
+            diag = Nk - N if int(causal) == 2 else 0
             for r0 in range(0, N, rows):
                 r1 = min(N, r0 + rows)
+                # keys any row of the block can see: j <= (r1 - 1) + diag
+                kc = min(Nk, max(0, r1 + diag)) if causal else Nk
+                if kc == 0:
+                    out[b, oi, r0:r1] = 0
+                    continue
                 qf = Q[b, h, r0:r1].astype(np.float32)
-                S = (qf @ kt) * sc
+                S = (qf @ kt[:, :kc]) * sc
                 mask = causal_mask(N, Nk, causal, r0, r1 - r0)
                 if mask is not None:
-                    S[mask] = -np.inf
+                    S[mask[:, :kc]] = -np.inf
                 if vis is not None:
-                    S[~vis[b, h, r0:r1]] = -np.inf
+                    S[~vis[b, h, r0:r1, :kc]] = -np.inf
                 P = _softmax_rows_f32(S)
-                o = P @ vf
+                o = P @ vf[:kc]
                 out[b, oi, r0:r1] = o if return_f32 else o.astype(np.float16)
     return out
 

@@ -249,6 +249,9 @@ def test_graph_capture_replays(device, masked):
     (1, 4, 4, 150, 300, 64, True, "bhqk"),
     (2, 8, 2, 333, 333, 128, "bottom_right", "qk"),
     (1, 2, 1, 257, 129, 64, False, "b1qk"),
+    # key padding broadcast over heads and rows (mask row stride 0)
+    (2, 4, 2, 180, 260, 64, True, "b11k"),
+    (2, 8, 4, 300, 300, 128, "bottom_right", "b11k"),
 ])
 def test_backward_with_mask(device, dtype, B, Hq, Hkv, Nq, Nk, D, causal, mshape):
     """Boolean attn_mask (broadcast over batch/heads/rows as given), combined
@@ -256,10 +259,15 @@ def test_backward_with_mask(device, dtype, B, Hq, Hkv, Nq, Nk, D, causal, mshape
     autograd Function."""
     print(f"[bwd mask] {dtype} B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} "
           f"causal={causal} mask={mshape}", flush=True)
-    shape = {"b1qk": (B, 1, Nq, Nk), "bhqk": (B, Hq, Nq, Nk), "qk": (Nq, Nk)}[mshape]
+    shape = {"b1qk": (B, 1, Nq, Nk), "bhqk": (B, Hq, Nq, Nk), "qk": (Nq, Nk),
+             "b11k": (B, 1, 1, Nk)}[mshape]
     g = torch.Generator("cpu").manual_seed(50)
     mask = torch.rand(*shape, generator=g) < 0.7
-    mask[..., 5, :] = False  # a row that sees no key
+    padding = mshape == "b11k"
+    if padding:
+        mask[0, ..., Nk - 40:] = False  # batch 0 right-padded by 40 keys
+    else:
+        mask[..., 5, :] = False  # a row that sees no key
     q, k, v = seeded((B, Hq, Nq, D), 51, dtype), seeded((B, Hkv, Nk, D), 52, dtype), \
         seeded((B, Hkv, Nk, D), 53, dtype)
     do = seeded((B, Hq, Nq, D), 54, dtype)
@@ -269,7 +277,11 @@ def test_backward_with_mask(device, dtype, B, Hq, Hkv, Nq, Nk, D, causal, mshape
     torch.cuda.synchronize()
     want = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=CODE[causal],
                                       attn_mask=mask.numpy())
-    assert torch.count_nonzero(leaves[0].grad[:, :, 5]) == 0
+    if not padding:
+        assert torch.count_nonzero(leaves[0].grad[:, :, 5]) == 0
+    else:  # keys hidden from every row get no gradient
+        assert torch.count_nonzero(leaves[1].grad[0, :, Nk - 40:]) == 0
+        assert torch.count_nonzero(leaves[2].grad[0, :, Nk - 40:]) == 0
     assert_grads([l.grad for l in leaves], want, dtype, f"mask {mshape}")
 
 

@@ -130,3 +130,43 @@ def test_separate_kv_length_matches_binding(device, lib, causal):
     expect = _C.flash_attention_forward_ex(q, k, v, causal, 0.125, False)[0]
     torch.cuda.synchronize()
     assert torch.equal(o, expect)
+
+
+def test_decode_mask_span_over_2gib(device, lib):
+    """A split-K-eligible call (group * Nq <= 32) whose mask strides span more
+    than the split-K kernel's 32-bit mask window: head 1's words sit 2 GiB
+    past head 0's.  The call must run on the prefill kernel (64-bit mask
+    addresses) and give the same result as the packed, contiguous mask."""
+    from flash_attention_sm75 import flash_attention_forward_ex
+
+    B, Hq, Hkv, Nq, Nk, D = 1, 2, 1, 1, 1000, 64
+    words = (Nk + 63) // 64
+    msh = (1 << 28) + 64  # words: 2 GiB + 512 bytes between the heads' rows
+    print(f"[decode mask span] head stride {msh * 8} bytes", flush=True)
+    g = torch.Generator("cpu").manual_seed(70)
+    q, k, v = (torch.randn(B, h, n, D, generator=g).half().to(device)
+               for h, n in ((Hq, Nq), (Hkv, Nk), (Hkv, Nk)))
+    vis = torch.rand(B, Hq, Nq, Nk, generator=g) < 0.6
+    packed = torch.zeros(Hq, words, dtype=torch.int64)
+    for h in range(Hq):
+        bits = vis[0, h, 0].tolist() + [False] * (64 * words - Nk)
+        for w in range(words):
+            word = sum(1 << i for i in range(64) if bits[64 * w + i])
+            packed[h, w] = word - (1 << 64) if word >= (1 << 63) else word
+    big = torch.zeros(msh * (Hq - 1) + words, dtype=torch.int64, device=device)
+    for h in range(Hq):
+        big[h * msh:h * msh + words] = packed[h].to(device)
+    o = torch.empty_like(q)
+    p = Params()
+    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    p.batch, p.heads_q, p.heads_kv, p.seq_len, p.seq_len_kv, p.head_dim = B, Hq, Hkv, Nq, Nk, D
+    lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+    p.scale, p.causal = 0.125, 0
+    p.mask_bits = big.data_ptr()
+    p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = 0, msh, words
+    p.stream = torch.cuda.current_stream().cuda_stream
+    assert lib.fa_sm75_forward(ctypes.byref(p)) == 0, lib.fa_sm75_last_error()
+    want = flash_attention_forward_ex(q, k, v, scale=0.125, attn_mask=vis.to(device))
+    torch.cuda.synchronize()
+    del big
+    torch.testing.assert_close(o, want, atol=2e-3, rtol=1e-2)

@@ -79,3 +79,37 @@ def test_tiny_qwen2_on_cpu_is_unchanged(patched):
         sp.apply_patch()
     assert torch.equal(patched_logits, plain)
     assert sp._stats["fallback_reasons"].get("not_cuda") == 2
+
+
+class _DeviceTensor:
+    """Stand-in for a device tensor in the eligibility check (no GPU here):
+    the shape, dtype and device facts _fallback_reason reads."""
+
+    def __init__(self, *shape, dtype=torch.float16):
+        self.shape, self.dtype, self.is_cuda = torch.Size(shape), dtype, True
+
+    def dim(self):
+        return len(self.shape)
+
+    def size(self, i):
+        return self.shape[i]
+
+
+@pytest.mark.parametrize("kwargs,reason", [({}, "gqa_not_enabled"),
+                                           ({"enable_gqa": False}, "gqa_not_enabled"),
+                                           ({"enable_gqa": True}, None)])
+def test_grouped_heads_need_enable_gqa(kwargs, reason):
+    """torch's SDPA rejects Hq != Hkv unless enable_gqa=True, so the patch
+    must not silently compute grouped-query attention for such a call."""
+    q, k = _DeviceTensor(1, 8, 16, 64), _DeviceTensor(1, 2, 16, 64)
+    assert sp._fallback_reason(q, k, k, None, 0.0, False, kwargs) == reason
+    same = _DeviceTensor(1, 8, 16, 64)
+    assert sp._fallback_reason(q, same, same, None, 0.0, False, {}) is None
+
+
+def test_gqa_without_enable_gqa_raises_like_torch(patched):
+    q, k = torch.randn(1, 4, 3, 64), torch.randn(1, 2, 3, 64)
+    with pytest.raises(RuntimeError):
+        sp._original_sdpa(q, k, k)
+    with pytest.raises(RuntimeError):
+        F.scaled_dot_product_attention(q, k, k)
