@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <atomic>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "fa_internal.h"
@@ -305,6 +306,47 @@ int validate_bwd(const fa_bwd_params* p) {
 
 }  // namespace
 
+// Scratch of fa_sm75_forward_noalloc: the split-K partials or the dynamic
+// schedule's queue counters that fa_sm75_forward otherwise takes from the
+// caller's workspace.  Each GPU the library runs on holds its own copy until
+// the process ends.  Host code never names this array as an address (its
+// name is a host-side stand-in there): it uses the per-device pointer from
+// hipGetSymbolAddress below.
+static __device__ __align__(256) unsigned char scratch[FA_SM75_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+
+// The current device's copy of `scratch`, looked up once per device (with
+// that device current) and kept.
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FA_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(FA_ERR_INVALID_ARGUMENT, "device %d is beyond the %d devices the scratch covers",
+                dev, kMaxScratchDevices);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || ptr == nullptr)
+        return fail(FA_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                    hipGetErrorString(e));
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return FA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 void fa_sm75_set_contiguous_strides(fa_fwd_params* p) {
@@ -352,6 +394,29 @@ int64_t fa_sm75_workspace_size(const fa_fwd_params* p) {
         .workspace_bytes;
   // Fused kernel: the counters of the dynamic schedule, when it would run.
   return fa::fused_workspace_bytes(a, (int)p->batch, (int)p->head_dim, p->causal != 0, policy);
+}
+
+int fa_sm75_forward_noalloc(const fa_fwd_params* p) {
+  g_last_error[0] = '\0';
+  const int st = validate(p, true);
+  if (st != FA_OK) return st;
+  if (p->workspace != nullptr || p->workspace_bytes != 0)
+    return fail(FA_ERR_INVALID_ARGUMENT,
+                "fa_sm75_forward_noalloc takes no workspace (workspace must be NULL and "
+                "workspace_bytes 0): it uses the library's own scratch");
+  if (p->batch == 0 || p->heads_q == 0 || p->seq_len == 0) return FA_OK;
+  const int64_t need = fa_sm75_workspace_size(p);
+  if (need > (int64_t)FA_SM75_NOALLOC_SCRATCH_BYTES)
+    return fail(FA_ERR_TOO_LARGE,
+                "this call needs %lld bytes of scratch; fa_sm75_forward_noalloc holds %lld",
+                (long long)need, (long long)FA_SM75_NOALLOC_SCRATCH_BYTES);
+  void* ptr = nullptr;
+  const int sst = scratch_of_current_device(&ptr);
+  if (sst != FA_OK) return sst;
+  fa_fwd_params q = *p;
+  q.workspace = ptr;
+  q.workspace_bytes = (int64_t)FA_SM75_NOALLOC_SCRATCH_BYTES;
+  return fa_sm75_forward(&q);
 }
 
 int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,

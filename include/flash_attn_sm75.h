@@ -125,6 +125,26 @@ int fa_sm75_forward(const fa_fwd_params* p);
  * counterpart (the reference has no decode path). */
 int64_t fa_sm75_workspace_size(const fa_fwd_params* p);
 
+/* Bytes of device scratch fa_sm75_forward_noalloc holds per GPU: the largest
+ * workspace fa_sm75_workspace_size() can ask for (split-K partials of at most
+ * 510 workgroups x 32 query rows x (128 + 2) floats, 8486400 bytes), rounded
+ * up to 8.5 MiB. */
+#define FA_SM75_NOALLOC_SCRATCH_BYTES (17u << 19)
+
+/* fa_sm75_forward without a caller workspace and without any allocation: the
+ * split-K partials or the dynamic schedule's counters live in one static
+ * device array of FA_SM75_NOALLOC_SCRATCH_BYTES per GPU, which the library
+ * holds until the process ends.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  p->workspace must
+ * be NULL and p->workspace_bytes 0; a call whose fa_sm75_workspace_size()
+ * exceeds the scratch returns FA_ERR_TOO_LARGE.  Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU (different streams, or
+ * threads) race; calls ordered on one stream do not.  Results are bitwise
+ * those of fa_sm75_forward with a workspace of fa_sm75_workspace_size(p)
+ * bytes.  Returns FA_OK or an fa_status. */
+int fa_sm75_forward_noalloc(const fa_fwd_params* p);
+
 /* Packs a boolean mask (one byte per element, nonzero = visible) of shape
  * [batch, heads, rows, cols] with element strides (any, 0 included) into the
  * bit layout of fa_fwd_params.mask_bits: out is [batch, heads, rows, words]

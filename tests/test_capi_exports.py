@@ -49,7 +49,8 @@ def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("fa_sm75_forward", "fa_sm75_naive_forward", "fa_sm75_last_error",
               "fa_sm75_status_string", "fa_sm75_abi_version", "fa_sm75_set_contiguous_strides",
-              "fa_sm75_workspace_size", "fa_sm75_pack_mask", "fa_sm75_backward",
+              "fa_sm75_workspace_size", "fa_sm75_forward_noalloc", "fa_sm75_pack_mask",
+              "fa_sm75_backward",
               "fa_sm75_backward_workspace_size", "fa_sm75_set_contiguous_bwd_strides",
               "launch_flash_attention_forward", "launch_flash_attention_forward_scalar",
               "launch_flash_attention_forward_wmma_qk", "launch_naive_attention"):
@@ -112,6 +113,23 @@ def test_validation_errors(lib, kw, status, msg):
     assert lib.fa_sm75_forward(ctypes.byref(p)) == status
     assert msg in lib.fa_sm75_last_error()
     assert lib.fa_sm75_status_string(status) != b"unknown status"
+
+
+def test_noalloc_validation(lib):
+    """fa_sm75_forward_noalloc validates like fa_sm75_forward and rejects a
+    caller workspace, all before touching the device."""
+    lib.fa_sm75_forward_noalloc.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_forward_noalloc.restype = ctypes.c_int
+    assert lib.fa_sm75_forward_noalloc(None) == 1
+    p = make(lib, head_dim=96)
+    assert lib.fa_sm75_forward_noalloc(ctypes.byref(p)) == 2
+    assert b"supports head_dim=64 or 128, got 96" in lib.fa_sm75_last_error()
+    p = make(lib, workspace=0x10000, workspace_bytes=4096)
+    assert lib.fa_sm75_forward_noalloc(ctypes.byref(p)) == 1
+    assert b"takes no workspace" in lib.fa_sm75_last_error()
+    p = make(lib, workspace_bytes=16)
+    assert lib.fa_sm75_forward_noalloc(ctypes.byref(p)) == 1
+    assert lib.fa_sm75_forward_noalloc(ctypes.byref(make(lib, seq_len=0))) == 0
 
 
 def test_null_params(lib):

@@ -1,0 +1,111 @@
+"""fa_sm75_forward_noalloc: the forward with the library's own static scratch
+instead of a caller workspace (needs a GPU).
+
+Checked through the C ABI against fa_sm75_forward given a workspace of
+fa_sm75_workspace_size() bytes: bitwise equal outputs and LSE, on two calls
+in a row where the second is smaller (the scratch keeps the first call's
+contents), for the two paths that use scratch: the split-K decode kernel
+(partials) and the fused kernel's dynamic schedule (queue counters).
+"""
+import ctypes
+
+import pytest
+import torch
+
+from capi_types import LIB, Params
+
+pytestmark = pytest.mark.gpu
+
+FA_OK, FA_ERR_INVALID_ARGUMENT = 0, 1
+FA_POLICY_AUTO, FA_POLICY_DYNAMIC = 0, 3
+
+
+@pytest.fixture(scope="module")
+def lib():
+    lib = ctypes.CDLL(LIB)
+    for n in ("fa_sm75_forward", "fa_sm75_forward_noalloc"):
+        getattr(lib, n).argtypes = [ctypes.POINTER(Params)]
+        getattr(lib, n).restype = ctypes.c_int
+    lib.fa_sm75_workspace_size.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_workspace_size.restype = ctypes.c_int64
+    lib.fa_sm75_set_contiguous_strides.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_last_error.restype = ctypes.c_char_p
+    lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
+    lib.fa_sm75_set_kernel_policy.restype = ctypes.c_int
+    return lib
+
+
+def call_pair(lib, device, B, Hq, Hkv, Nq, Nk, D, causal, seed):
+    """Runs one problem through both entry points; returns the two (O, LSE)
+    pairs and the workspace size the call asks for."""
+    print(f"[noalloc] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} causal={causal}",
+          flush=True)
+    g = torch.Generator("cpu").manual_seed(seed)
+    q = torch.randn(B, Hq, Nq, D, generator=g).half().to(device)
+    k = torch.randn(B, Hkv, Nk, D, generator=g).half().to(device)
+    v = torch.randn(B, Hkv, Nk, D, generator=g).half().to(device)
+    outs = []
+    need = None
+    for entry in ("fa_sm75_forward", "fa_sm75_forward_noalloc"):
+        o = torch.full_like(q, float("nan"))
+        lse = torch.full((B, Hq, Nq), float("nan"), dtype=torch.float32, device=device)
+        p = Params()
+        p.q, p.k, p.v, p.o, p.lse = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                     lse.data_ptr())
+        p.batch, p.heads_q, p.heads_kv, p.seq_len, p.seq_len_kv, p.head_dim = (
+            B, Hq, Hkv, Nq, Nk, D)
+        lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+        p.scale, p.causal = D ** -0.5, causal
+        p.stream = torch.cuda.current_stream().cuda_stream
+        ws = None
+        if entry == "fa_sm75_forward":
+            need = lib.fa_sm75_workspace_size(ctypes.byref(p))
+            ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+            p.workspace, p.workspace_bytes = ws.data_ptr(), need
+        rc = getattr(lib, entry)(ctypes.byref(p))
+        assert rc == FA_OK, (entry, lib.fa_sm75_last_error())
+        torch.cuda.synchronize()
+        del ws
+        outs.append((o, lse))
+    return outs, need
+
+
+def assert_same(outs):
+    (o1, l1), (o2, l2) = outs
+    assert torch.equal(o1, o2)
+    assert torch.equal(l1, l2)
+    assert not torch.isnan(o2).any()
+
+
+def test_split_k_partials_in_scratch(device, lib):
+    # group * Nq <= 32: split-K decode; the partials go to the scratch
+    outs, need = call_pair(lib, device, 2, 32, 8, 1, 4096, 128, 0, seed=1)
+    assert need > 0
+    assert_same(outs)
+    outs, need2 = call_pair(lib, device, 1, 8, 2, 3, 700, 64, 2, seed=2)  # smaller
+    assert 0 < need2 < need
+    assert_same(outs)
+
+
+def test_dynamic_schedule_counters_in_scratch(device, lib):
+    assert lib.fa_sm75_set_kernel_policy(FA_POLICY_DYNAMIC) == FA_OK
+    try:
+        outs, need = call_pair(lib, device, 1, 16, 4, 2048, 2048, 128, 1, seed=3)
+        assert need > 0
+        assert_same(outs)
+        outs, _ = call_pair(lib, device, 1, 8, 8, 700, 700, 64, 1, seed=4)  # smaller
+        assert_same(outs)
+    finally:
+        lib.fa_sm75_set_kernel_policy(FA_POLICY_AUTO)
+
+
+def test_rejects_a_workspace(device, lib):
+    q = torch.zeros(1, 2, 64, 64, dtype=torch.float16, device=device)
+    p = Params()
+    p.q = p.k = p.v = p.o = q.data_ptr()
+    p.batch, p.heads_q, p.heads_kv, p.seq_len, p.head_dim = 1, 2, 2, 64, 64
+    lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+    p.scale = 0.125
+    p.workspace, p.workspace_bytes = q.data_ptr(), 1024
+    assert lib.fa_sm75_forward_noalloc(ctypes.byref(p)) == FA_ERR_INVALID_ARGUMENT
+    assert b"takes no workspace" in lib.fa_sm75_last_error()
