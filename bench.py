@@ -149,6 +149,8 @@ def kernel_stats(cfg, kern_ms):
         "frac": round(F / (avg * 1e-3) / 1e12 / PEAK_TFLOPS, 4),
         "flop": F,
         "launches": len(kern_ms),
+        "traffic": read_traffic(cfg),
+        "algorithmic_bytes": min_bytes(B, Hq, Hkv, N, D),
     }
 
 
