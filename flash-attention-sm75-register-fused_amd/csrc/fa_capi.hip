@@ -365,7 +365,7 @@ int fa_sm75_forward(const fa_fwd_params* p) {
   const fa::FwdArgs a = make_args(p);
   const int policy = g_kernel_policy.load(std::memory_order_relaxed);
   const hipStream_t stream = reinterpret_cast<hipStream_t>(p->stream);
-  if (policy == FA_POLICY_AUTO && fa::decode_eligible(a)) {
+  if (policy == FA_POLICY_AUTO && fa::decode_eligible(a, (int)p->batch)) {
     const int64_t room = p->workspace != nullptr ? p->workspace_bytes : 0;
     const fa::DecodePlan plan =
         fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, room);
@@ -389,7 +389,7 @@ int64_t fa_sm75_workspace_size(const fa_fwd_params* p) {
   if (st != FA_OK || p->batch == 0 || p->heads_q == 0 || p->seq_len == 0) return 0;
   const fa::FwdArgs a = make_args(p);
   const int policy = g_kernel_policy.load(std::memory_order_relaxed);
-  if (policy == FA_POLICY_AUTO && fa::decode_eligible(a))
+  if (policy == FA_POLICY_AUTO && fa::decode_eligible(a, (int)p->batch))
     return fa::plan_decode(a, (int)p->batch, (int)p->head_dim, p->causal != 0, INT64_MAX)
         .workspace_bytes;
   // Fused kernel: the counters of the dynamic schedule, when it would run.

@@ -18,11 +18,18 @@
 //     writes an fp32 partial (unnormalised O, running max in log2 units, sum)
 //     to the caller's workspace and fa_decode_combine merges the splits.
 //
+// Small launches (a 128-row prefill grid of at most kSmallLaunchItems
+// workgroups, e.g. one head of 512 rows) take the same path with the query
+// rows of each (batch, KV head) in blocks of 32: a unit is then one such
+// block, and its keys are split over workgroups like a decode unit's, so the
+// launch spreads over many CUs instead of running a few long key chains.
+//
 // The MFMA formulation, the LDS tile layout, the online-softmax numerics and
 // the lazy rescale are those of the prefill kernel (fa_fwd.hip): S^T = K Q^T
 // with one query per lane, P kept in registers as the B operand of
-// O^T = V^T P^T.  Query column r of unit (b, hkv) is query head
-// hkv * group + r / Nq, query index r % Nq.
+// O^T = V^T P^T.  Query column c of unit (b, hkv, row block rb) is row
+// r = 32 rb + c of the (batch, KV head): query head hkv * group + r / Nq,
+// query index r % Nq.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -36,7 +43,14 @@ namespace fa {
 namespace {
 
 constexpr int kDecTile = 32;       // keys per wave tile
-constexpr int kDecMinTiles = 8;    // fewest tiles a split is given
+constexpr int kDecMinTiles = 8;    // fewest tiles a split is given (decode)
+constexpr int kSmallMinTiles = 4;  // small launches: one tile per wave
+// Small launches with at most this many 32-key tiles run one split per unit:
+// the four waves of the workgroup (16 tiles each at most) are then the whole
+// key split, and the launch needs neither a workspace nor the combine kernel
+// (whose launch costs more than it saves on such short key ranges; measured
+// on MI355X: one head of 512 rows 6.3 against 8.9 us, of 2048 rows even).
+constexpr int kSmallNoSplitTiles = 64;
 constexpr int kDecTargetWgs = 256; // one workgroup per CU (measured best)
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -89,16 +103,30 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   const int unit = (int)blockIdx.x / d.splits;
   const int split = (int)blockIdx.x - unit * d.splits;
   const int hkv_count = a.hq / a.group;
-  const int b = unit / hkv_count;
-  const int hkv = unit - b * hkv_count;
+  const int bh = unit / d.row_blocks;  // (batch, KV head)
+  const int rb = unit - bh * d.row_blocks;
+  const int b = bh / hkv_count;
+  const int hkv = bh - b * hkv_count;
   const int nq = a.n;
   const int NK = a.nk;
 
-  // This lane's query column.
-  const bool row_ok = ql < d.rows;
-  const int g = ql / nq;
-  const int qi = ql - g * nq;
+  // This lane's query column: row r of the (batch, KV head).
+  const int r = rb * kDecodeMaxRows + ql;
+  const bool row_ok = ql < d.rows && r < d.total_rows;
+  const int g = r / nq;
+  const int qi = r - g * nq;
   const int hq = hkv * a.group + g;
+  // Smallest query index of the block's rows (wave-uniform): causal tiles
+  // past it + diag need the per-element mask.
+  const int r0 = rb * kDecodeMaxRows;
+  const int r_last = min(d.total_rows, r0 + kDecodeMaxRows) - 1;
+  const bool one_head = r0 / nq == r_last / nq;
+  const int qi_lo = one_head ? r0 % nq : 0;
+  // Largest query index of the block's rows: under causal masking no row of
+  // the unit sees a key past qi_hi + diag, so tiles past it are skipped.
+  const int qi_hi = one_head ? r_last % nq : nq - 1;
+  const int unit_tiles =
+      CAUSAL ? min(d.tiles, max(0, (qi_hi + a.diag + kDecTile) / kDecTile)) : d.tiles;
 
   half8 qf[KK];
   if (row_ok) {
@@ -116,7 +144,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
 
   // Tiles of this split, and this wave's share (every fourth one).
   const int t_begin = split * d.chunk_tiles;
-  const int t_end = min(t_begin + d.chunk_tiles, d.tiles);
+  const int t_end = min(t_begin + d.chunk_tiles, unit_tiles);
   const int nt_w = t_end - t_begin > wave ? (t_end - t_begin - wave + kWaves - 1) / kWaves : 0;
   const int key0 = t_begin * kDecTile;
   const _Float16* Kp = a.k + b * a.ksb + hkv * a.ksh;
@@ -220,7 +248,8 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
       s = E::mfma(kc[kk], qf[kk], s);
 
     const int kstart = key0 + (wave + kWaves * it) * kDecTile;
-    bool need_mask = (kstart + kDecTile > NK) || (CAUSAL && kstart + kDecTile - 1 > a.diag);
+    bool need_mask =
+        (kstart + kDecTile > NK) || (CAUSAL && kstart + kDecTile - 1 > qi_lo + a.diag);
     if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
     if (need_mask) {
       const uint32_t mws = mw >> (4 * hi);  // bit 8 (i / 4) + i % 4: element i
@@ -375,14 +404,18 @@ __global__ void __launch_bounds__(kCombineThreads) fa_decode_combine(const DecAr
   __shared__ float o_part[GROUPS][D];
   const int tid = threadIdx.x;
   const int unit = (int)blockIdx.x / d.rows;
-  const int r = (int)blockIdx.x - unit * d.rows;
+  const int c = (int)blockIdx.x - unit * d.rows;  // query column of the unit
   const int hkv_count = a.hq / a.group;
-  const int b = unit / hkv_count;
-  const int hkv = unit - b * hkv_count;
+  const int bh = unit / d.row_blocks;
+  const int rb = unit - bh * d.row_blocks;
+  const int b = bh / hkv_count;
+  const int hkv = bh - b * hkv_count;
+  const int r = rb * kDecodeMaxRows + c;
+  if (r >= d.total_rows) return;  // whole workgroup: columns past the last row
   const int g = r / a.n;
   const int qi = r - g * a.n;
   const int hq = hkv * a.group + g;
-  const int64_t p0 = (int64_t)unit * d.splits * d.rows + r;  // split s: p0 + s * rows
+  const int64_t p0 = (int64_t)unit * d.splits * d.rows + c;  // split s: p0 + s * rows
   const int S = d.splits;
 
   // maximum over the splits
@@ -472,8 +505,10 @@ void launch_decode_typed(const DecArgs& d, const DecodePlan& pl, int head_dim, b
 
 }  // namespace
 
-bool decode_eligible(const FwdArgs& a) {
-  if ((int64_t)a.group * a.n > kDecodeMaxRows) return false;
+bool decode_eligible(const FwdArgs& a, int batch) {
+  const bool decode = (int64_t)a.group * a.n <= kDecodeMaxRows;
+  const int64_t prefill_items = (int64_t)batch * a.hq * ((a.n + 127) / 128);
+  if (!decode && prefill_items > kSmallLaunchItems) return false;
   if (a.mbits != nullptr) {
     // The split-K kernel reads one batch's mask rows through a single 32-bit
     // buffer window (byte offsets up to this span); a call whose mask strides
@@ -490,15 +525,19 @@ bool decode_eligible(const FwdArgs& a) {
 DecodePlan plan_decode(const FwdArgs& a, int batch, int head_dim, bool causal,
                        int64_t workspace_bytes) {
   DecodePlan pl;
-  pl.rows = a.group * a.n;
-  pl.units = batch * (a.hq / a.group);
+  pl.total_rows = a.group * a.n;
+  pl.rows = std::min(pl.total_rows, kDecodeMaxRows);
+  pl.row_blocks = (pl.total_rows + kDecodeMaxRows - 1) / kDecodeMaxRows;
+  pl.units = batch * (a.hq / a.group) * pl.row_blocks;
   // Keys any query row can see.
   int64_t nk_eff = a.nk;
   if (causal) nk_eff = std::min<int64_t>(a.nk, std::max<int64_t>(0, (int64_t)a.n + a.diag));
   pl.tiles = (int)((nk_eff + kDecTile - 1) / kDecTile);
   int splits = std::min((kDecTargetWgs + pl.units - 1) / pl.units, kMaxSplits);
-  splits = std::min(splits, std::max(1, pl.tiles / kDecMinTiles));
+  splits = std::min(
+      splits, std::max(1, pl.tiles / (pl.row_blocks > 1 ? kSmallMinTiles : kDecMinTiles)));
   splits = std::max(splits, 1);
+  if (pl.row_blocks > 1 && pl.tiles <= kSmallNoSplitTiles) splits = 1;
   pl.chunk_tiles = std::max(1, (pl.tiles + splits - 1) / splits);
   pl.splits = std::max(1, (pl.tiles + pl.chunk_tiles - 1) / pl.chunk_tiles);
   pl.workspace_bytes =
@@ -516,6 +555,8 @@ int launch_decode_forward(const FwdArgs& a, const DecodePlan& pl, int head_dim, 
   DecArgs d;
   d.f = a;
   d.rows = pl.rows;
+  d.total_rows = pl.total_rows;
+  d.row_blocks = pl.row_blocks;
   d.splits = pl.splits;
   d.chunk_tiles = pl.chunk_tiles;
   d.tiles = pl.tiles;

@@ -354,12 +354,18 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       return fmaxf(m0, m1);
     };
     float mc = 0.0f;  // running max of tile j's rows, times c2 (exp2 offset)
+    // A row outgrew its running max by more than 2^kRescaleLog2 iff its max
+    // score exceeds thr = m_run + kRescaleLog2 / c2 (-inf before any key).
+    float thr = -__builtin_inff();
 
     // Prepares tile j's scores for its softmax: masks them if tile j crosses
     // the sequence end or this wave's causal diagonal, or (MASK) hides a key
-    // from some row of the wave (the unmasked row max mx is then recomputed),
-    // raises the running max when some row outgrew it by more than
-    // 2^kRescaleLog2 (rescaling O and l), and sets mc.  mw: the lane's mask
+    // from some row of the wave (the unmasked max mx is then recomputed),
+    // and raises the running max when some row outgrew it by more than
+    // 2^kRescaleLog2 (rescaling O and l, and updating mc and thr).  mx: the
+    // lane's max over its half of the row (the two wave halves hold the
+    // row's other 16 keys of each 32-key sub-tile; the threshold test needs
+    // no exchange between them, the rare rescale does).  mw: the lane's mask
     // word of tile j (bit k: key 64 j + k visible).
     auto prepare = [&](int j, float16v (&s)[2], float mx, uint64_t mw) {
       const int kstart = j * kBlockN;
@@ -368,21 +374,24 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
       if (need_mask) {
         const uint64_t mws = mw >> (4 * hi);  // bit 32 t + 8 (i / 4) + i % 4: element (t, i)
+        // Element (t, i) holds key kstart + 4 hi + off, off = 32 t + 8 (i / 4)
+        // + i % 4 (a constant); it is visible iff off <= lim.
+        const int last = CAUSAL ? min(NK - 1, qrow + a.diag) : NK - 1;
+        const int lim = last - kstart - 4 * hi;
         // static_for: a loop the unroller leaves rolled would index s at run
         // time and move the score registers to scratch memory.
         static_for<32>([&](auto e_c) {
           constexpr int e = decltype(e_c)::value;
           constexpr int t = e >> 4, i = e & 15;
-          const int key = kstart + 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);
-          bool masked = (key >= NK) || (CAUSAL && key > qrow + a.diag);
-          if (MASK) masked = masked || ((mws >> (32 * t + 8 * (i >> 2) + (i & 3))) & 1) == 0;
+          constexpr int off = 32 * t + 8 * (i >> 2) + (i & 3);
+          bool masked = off > lim;
+          if (MASK) masked = masked || ((mws >> off) & 1) == 0;
           if (masked) s[t][i] = -__builtin_inff();
         });
-        mx = halves_max(row_max(s));
+        mx = row_max(s);
       }
-      const bool grow = (mx - m_run) * c2 > kRescaleLog2;
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float m_new = fmaxf(m_run, mx);
+      if (__builtin_amdgcn_ballot_w64(mx > thr) != 0) {
+        const float m_new = fmaxf(m_run, halves_max(mx));
         const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
         const float alpha =
             (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * c2);
@@ -390,8 +399,9 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) oacc[mt] *= alpha;
         m_run = m_new;
+        mc = m_use * c2;
+        thr = m_new + kRescaleLog2 / c2;
       }
-      mc = ((m_run == -__builtin_inff()) ? 0.0f : m_run) * c2;
     };
 
     // One pipeline step for tile j, at position U of the unrolled loop (its
@@ -454,9 +464,9 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         const int last_ok = PV_FIRST + (p / 4) * MT - 1;
         return spread < last_ok ? spread : last_ok;
       };
-      // Row max of S_{j+1}: element e (sub-tile t = e / 16) is folded in at
-      // max_slot(e), a few slots after the last MFMA into sub-tile t; the lane
-      // swap of the two wave halves sits in the last slot.
+      // Row max of S_{j+1} over the lane's half of the row: element e
+      // (sub-tile t = e / 16) is folded in at max_slot(e), a few slots after
+      // the last MFMA into sub-tile t.
       constexpr auto max_slot = [](int e) constexpr {
         const int t = e >> 4, i = e & 15;
         const int first = (t + 1) * KK + 2;
@@ -522,7 +532,6 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
             constexpr int e = decltype(e_c)::value;
             if constexpr (max_slot(e) == slot) mx_next = fmaxf(mx_next, s_nxt[e >> 4][e & 15]);
           });
-          if constexpr (slot == NB - 1) mx_next = halves_max(mx_next);
         }
         static_for<16>([&](auto p_c) {
           if constexpr (pair_slot(decltype(p_c)::value) == slot) softmax_pair(p_c);
@@ -560,7 +569,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         for (int kk = 0; kk < KK; ++kk)
           s_buf[0][t] = E::mfma(read_k(k_first, t * KK + kk), qf[kk], s_buf[0][t]);
       }
-      prepare(tile0, s_buf[0], halves_max(row_max(s_buf[0])), MASK ? mrow[tile0] : ~0ull);
+      prepare(tile0, s_buf[0], row_max(s_buf[0]), MASK ? mrow[tile0] : ~0ull);
       // Step 0 loads K_STAGES into K_0's buffer: every wave must be done
       // reading it for S_0 first.
       __syncthreads();

@@ -93,12 +93,18 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
 bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy);
 int fused_block_m();  // rows of the smallest workgroup (grid-size checks)
 
-// Split-K path for few query rows per K/V head (fa_decode.hip): taken when
-// heads_q / heads_kv * seq_len <= kDecodeMaxRows.
+// Split-K path (fa_decode.hip): taken when heads_q / heads_kv * seq_len <=
+// kDecodeMaxRows (KV-cache decode: all query rows of one K/V head fit one
+// 32-column MFMA tile), and for small launches, whose 128-row prefill grid
+// would hold at most kSmallLaunchItems workgroups: their query rows then go
+// in blocks of 32, each block's keys split over several workgroups.
 constexpr int kDecodeMaxRows = 32;
+constexpr int kSmallLaunchItems = 64;
 struct DecArgs {
   FwdArgs f;
-  int rows;         // query columns per unit: group * n
+  int rows;         // query columns per unit: min(32, group * n)
+  int total_rows;   // query rows per (batch, KV head): group * n
+  int row_blocks;   // units per (batch, KV head): ceil(total_rows / 32)
   int splits;       // key ranges per unit
   int chunk_tiles;  // 32-key tiles per split
   int tiles;        // 32-key tiles any row can see
@@ -106,10 +112,10 @@ struct DecArgs {
   float* part_ml;   // [units, splits, rows, 2]: max (log2 units), sum
 };
 struct DecodePlan {
-  int rows, units, tiles, splits, chunk_tiles;
+  int rows, total_rows, row_blocks, units, tiles, splits, chunk_tiles;
   int64_t workspace_bytes;  // 0 when splits == 1
 };
-bool decode_eligible(const FwdArgs& a);
+bool decode_eligible(const FwdArgs& a, int batch);
 // Splits for a workspace of `workspace_bytes` (one split if it is too small).
 DecodePlan plan_decode(const FwdArgs& a, int batch, int head_dim, bool causal,
                        int64_t workspace_bytes);

@@ -119,9 +119,10 @@ def test_key_split_auto_picks_one(device):
 
 
 def test_kernels_agree_and_auto_picks_one(device):
-    """Auto mode equals one of the forced kernels bit for bit, on a large
-    causal launch (128-row kernel) and a small one (key-split kernel); the
-    forced kernels agree within rounding."""
+    """On a large causal launch auto mode equals one of the forced kernels bit
+    for bit; a small one (12 query blocks) runs the split-K small-launch path
+    (oracle-checked in test_gpu_small_launch.py) and agrees with them within
+    rounding; the forced kernels agree within rounding."""
     for (B, Hq, Hkv, N) in ((4, 32, 8, 1000), (1, 4, 4, 300)):
         q, k, v = (t.to(device) for t in inputs(B, Hq, Hkv, N, 128, seed=B * N))
         outs = {}
@@ -129,7 +130,12 @@ def test_kernels_agree_and_auto_picks_one(device):
             with policy(pol):
                 outs[pol] = flash_attention_forward(q, k, v, causal=True)
         torch.cuda.synchronize()
-        assert any(torch.equal(outs[0], outs[p]) for p in (NARROW, WIDE, SPLIT))
+        small = B * Hq * ((N + 127) // 128) <= 64
+        if small:
+            diff = (outs[0].float() - outs[NARROW].float()).abs().max().item()
+            assert diff < 4e-3, diff
+        else:
+            assert any(torch.equal(outs[0], outs[p]) for p in (NARROW, WIDE, SPLIT))
         for p in (WIDE, SPLIT):
             diff = (outs[NARROW].float() - outs[p].float()).abs().max().item()
             assert diff < 4e-3, (p, diff)
