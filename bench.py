@@ -15,9 +15,12 @@ of the dense fp16 MFMA peak (2.5 PFLOP/s).  The default workload is C4, the
 configuration the north-star target is quoted on (B=1 Hq=32 Hkv=8 N=8192
 D=128 causal).
 
-Printed: ONE JSON line on stdout (rank 0).  Besides the driver's keys it holds
-  roofline      the kernel's average launch time (HIP events around each
-                launch, on the launch stream) against the MFMA peak; traffic
+Printed: ONE JSON line on stdout (rank 0).  The timed region is K forward
+calls issued back to back between two synchronisations; value is the FLOP of
+those calls over its wall time.  Besides the driver's keys the line holds
+  roofline      the kernel's average launch time (one HIP event pair on the
+                launch stream around the timed region) against the MFMA
+                peak; traffic
                 is the HBM bytes per launch from the committed rocprofv3
                 FETCH_SIZE/WRITE_SIZE summary for this workload, when present;
                 sustained_mfma is a dense fp16 GEMM (hipBLASLt) on random
@@ -104,10 +107,16 @@ def read_traffic(cfg):
     return float(m.group(1)) if m else None
 
 
-def time_gpu(cfg, steps, warmup, data="randn", stream_avg=False, warm_ms=0.0):
-    """K timed launches of one configuration after W warm-up launches (and,
-    with warm_ms, at least that many milliseconds of launches: an idle GPU
-    takes some tens of milliseconds of load to reach its working clock)."""
+def time_gpu(cfg, steps, warmup, data="randn", warm_ms=0.0):
+    """Times one configuration: W warm-up launches (and, with warm_ms, at
+    least that many milliseconds of launches: an idle GPU takes some tens of
+    milliseconds of load to reach its working clock), then the timed region
+    -- K launches back to back, bracketed by synchronisations, with one HIP
+    event pair on the launch stream around them -- and after it K more
+    launches each between its own pair of events (the per-launch statistics
+    the reference's benchmark reports).  Returns (wall seconds of the timed
+    region, sorted per-launch ms, average ms per launch of the timed region
+    by its events)."""
     import torch
 
     from flash_attention_sm75 import flash_attention_forward
@@ -127,31 +136,25 @@ def time_gpu(cfg, steps, warmup, data="randn", stream_avg=False, warm_ms=0.0):
     for _ in range(warmup):
         flash_attention_forward(q, k, v, causal=causal)
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        ev[i][0].record(stream)
-        flash_attention_forward(q, k, v, causal=causal)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kern_ms = sorted(a.elapsed_time(b) for a, b in ev)
-    if not stream_avg:
-        return wall, kern_ms
-    # The same K launches back to back between one pair of events: the
-    # launch rate of a stream of calls, without the per-launch event records
-    # (which cost a few microseconds each, a sizeable share of a 20-30 us
-    # launch).
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
     e0.record(stream)
     for _ in range(steps):
         flash_attention_forward(q, k, v, causal=causal)
     e1.record(stream)
     torch.cuda.synchronize()
-    return wall, kern_ms, e0.elapsed_time(e1) / steps
+    wall = time.perf_counter() - t0
+    stream_ms = e0.elapsed_time(e1) / steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(stream)
+        flash_attention_forward(q, k, v, causal=causal)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    kern_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    return wall, kern_ms, stream_ms
 
 
 def kernel_stats(cfg, kern_ms, stream_ms):
@@ -551,17 +554,21 @@ def main():
         for c in sorted(k for k in CONFIGS if k.startswith("C")):
             if c == cfg:
                 continue
-            _, km, sm = time_gpu(c, args.steps, args.warmup, stream_avg=True, warm_ms=100.0)
+            _, km, sm = time_gpu(c, args.steps, args.warmup, warm_ms=100.0)
             per_config[c] = kernel_stats(c, km, sm)
 
-    wall, kern_ms, stream_ms = time_gpu(cfg, args.steps, args.warmup, args.data, stream_avg=True)
+    # Before the W warm-up steps, at least 200 ms of untimed launches: after
+    # a change of load the board's power management takes a few tens of
+    # launches to settle the clock (C4 per-launch traces: 574 -> 695 -> 560
+    # us over the first ~30 launches after the C5 timing).
+    wall, kern_ms, stream_ms = time_gpu(cfg, args.steps, args.warmup, args.data, warm_ms=200.0)
     ms_per_step = wall * 1e3 / args.steps
-    avg_kernel_ms = sum(kern_ms) / len(kern_ms)
+    avg_kernel_ms = stream_ms  # HIP events over the timed region, per launch
     value = F * args.steps / wall / 1e12
     achieved = F / (avg_kernel_ms * 1e-3) / 1e12
-    log(f"[{cfg}] wall {ms_per_step:.4f} ms/step, kernel avg {avg_kernel_ms:.4f} ms "
-        f"(median {kern_ms[len(kern_ms) // 2]:.4f}, min {kern_ms[0]:.4f}) -> "
-        f"{value:.1f} TFLOPS wall, {achieved:.1f} TFLOPS kernel")
+    log(f"[{cfg}] wall {ms_per_step:.4f} ms/step, kernel avg {avg_kernel_ms:.4f} ms (events over "
+        f"the timed region; per-launch events after it: median {kern_ms[len(kern_ms) // 2]:.4f}, "
+        f"min {kern_ms[0]:.4f}) -> {value:.1f} TFLOPS wall, {achieved:.1f} TFLOPS kernel")
 
     if run_configs:
         per_config[cfg] = kernel_stats(cfg, kern_ms, stream_ms)
