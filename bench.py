@@ -362,10 +362,12 @@ def time_sdpa_decode_call(keys, n=200):
     return out
 
 
-def time_backward(cfg, steps=10, warmup=3, dtype="fp16"):
+def time_backward(cfg, steps=10, warmup=3, dtype="fp16", warm_ms=200.0):
     """Average time of one flash_attention_backward call (stats, dK/dV and dQ
     kernels) on the workload's shape, HIP events on the launch stream around
-    the timed calls; inputs, O, LSE and dO resident in HBM."""
+    the timed calls, after W warm-up calls and at least warm_ms of them (the
+    clock settles after a change of load); inputs, O, LSE and dO resident in
+    HBM."""
     import torch
 
     from flash_attention_sm75 import flash_attention_backward, flash_attention_forward_ex
@@ -379,6 +381,11 @@ def time_backward(cfg, steps=10, warmup=3, dtype="fp16"):
     v = (torch.randn(B, Hkv, N, D, generator=g) * std).to(dt).to(dev)
     do = torch.randn(B, Hq, N, D, generator=g).to(dt).to(dev)
     o, lse = flash_attention_forward_ex(q, k, v, causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        flash_attention_backward(do, q, k, v, o, lse, causal=causal)
+        torch.cuda.synchronize()
     for _ in range(warmup):
         flash_attention_backward(do, q, k, v, o, lse, causal=causal)
     stream = torch.cuda.current_stream()
@@ -516,7 +523,7 @@ def main():
                 f"{flops(b_, hq_, n_, d_, ca_) / med / 1e9:.1f} TFLOPS")
             if not args.no_backward:
                 for dt in ("fp16", "bf16"):
-                    bms = time_backward(c, 5, 2, dt)
+                    bms = time_backward(c, 5, 2, dt, warm_ms=50.0)
                     log(f"[{c} backward {dt}] {bms:.4f} ms -> "
                         f"{2.5 * flops(b_, hq_, n_, d_, ca_) / bms / 1e9:.1f} TFLOPS (2.5x fwd FLOPs)")
 

@@ -147,9 +147,9 @@ __global__ void __launch_bounds__(256) fa_bwd_stats_kernel(const BwdArgs a) {
 }
 
 // ---- dK, dV ------------------------------------------------------------------
-// Step s of a workgroup: query head hkv * group + s / per_head, query tile
-// qt_begin + s % per_head (causal: the first tile with a query that sees one
-// of the block's keys), two 32-query sub-tiles each.
+// Step s of a workgroup: query head hkv * group + s % group, query tile
+// qtiles - 1 - s / group, down to qt_begin (causal: the first tile with a
+// query that sees one of the block's keys), two 32-query sub-tiles each.
 //
 // One wave per SIMD (128 accumulator, 64 operand VGPRs per lane; 123 KiB of
 // LDS), so the wave has to hide its own latencies: the loop is software
@@ -268,17 +268,24 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
     else if constexpr (S == 1) return m_lds1;
     else return m_lds2;
   };
+  // Step s takes query tile qtiles - 1 - s / group of query head s % group:
+  // tiles in descending order, every head of the group at each tile.  The
+  // key blocks running at once on an XCD (one KV head each) then all start
+  // at the last tile and walk down together, each stopping at its causal
+  // start, so they stream the same Q and dO tiles through the XCD's L2
+  // (measured +1% on the C4 training shape against head-major ascending).
   auto qbase_of = [&](int s) {
-    const int h = s / per_head;
-    return (qt_begin + (s - h * per_head)) * kBwdStatsTile;
+    const int j = s / a.group;
+    return (a.qtiles - 1 - j) * kBwdStatsTile;
   };
   // Direct loads of step s's Q and dO tiles (wave w: segments w, w+4, ..)
   // and, by wave 0, its stats record, into the buffers of stage ST.
   auto issue = [&](int s, auto st) {
     _Float16* const qdst = qbuf(st);
     _Float16* const ddst = dbuf(st);
-    const int h = s / per_head;
-    const int qt = qt_begin + (s - h * per_head);
+    const int j = s / a.group;
+    const int h = s - j * a.group;
+    const int qt = a.qtiles - 1 - j;
     const int hq = hkv * a.group + h;
     const int q0 = qt * kBwdStatsTile;
     const int rows = N - q0;
