@@ -34,7 +34,9 @@ those calls over its wall time.  Besides the driver's keys the line holds
                 stream), the average of K launches issued back to back, and
                 TFLOPS and the fraction of the MFMA peak from the latter;
   backward      the backward pass (dQ, dK, dV) on the same workload: its
-                average time and TFLOPS at 2.5x the forward's FLOP count.
+                average time and TFLOPS at 2.5x the forward's FLOP count;
+  decode        the split-K decode path (D1-D3: one query row per head
+                against a KV cache): median call time and HBM rate.
 Diagnostics go to stderr.
 """
 import argparse
@@ -318,6 +320,11 @@ def time_decode(name, steps=20, warmup=5, policy=0):
     v = torch.randn(B, Hkv, Nk, D, generator=g).half().to(dev)
     _C.set_kernel_policy(policy)
     try:
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) < 0.05:  # 50 ms of calls: settle the clock
+            for _ in range(10):
+                flash_attention_forward_ex(q, k, v)
+            torch.cuda.synchronize()
         for _ in range(warmup):
             flash_attention_forward_ex(q, k, v)
         stream = torch.cuda.current_stream()
@@ -474,6 +481,8 @@ def main():
                          "(the kernel is power-limited: less data toggling, higher clock)")
     ap.add_argument("--policy", type=int, default=0, choices=(0, 1, 2),
                     help="kernel policy: 0 auto, 1 = 128-row (4-wave), 2 = 256-row (8-wave)")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip timing the split-K decode workloads D1-D3")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip timing the other BASELINE configurations (C1-C5)")
     ap.add_argument("--no-backward", action="store_true",
@@ -610,6 +619,21 @@ def main():
         }
         log(f"[{cfg} backward] {backward}")
 
+    # The split-K decode path (KV-cache decode, HBM-bound): median time of a
+    # call (both kernels) and its rate against the 8 TB/s HBM peak.
+    decode = None
+    if not args.no_decode and args.data == "randn":
+        decode = {}
+        for c in sorted(DECODE_CONFIGS):
+            B_, Hq_, Hkv_, Nq_, Nk_, D_ = DECODE_CONFIGS[c]
+            ms, gbs = time_decode(c)
+            decode[c] = {
+                "workload": f"decode B={B_} Hq={Hq_} Hkv={Hkv_} Nq={Nq_} Nk={Nk_} d={D_}",
+                "median_ms": round(ms, 5), "gb_per_s": round(gbs, 1),
+                "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+            }
+        log(f"[decode] {decode}")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.cpu_budget)
@@ -650,6 +674,7 @@ def main():
         "configs": per_config or None,
         "cpu_baseline": cpu,
         "backward": backward,
+        "decode": decode,
     }
     print(json.dumps(line), flush=True)
 
