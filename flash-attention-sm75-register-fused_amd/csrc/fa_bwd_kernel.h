@@ -8,18 +8,22 @@
 //   dV = P^T dO,  dP = dO V^T,  dS = P o (dP - rowsum(dO o O)),
 //   dQ = scale * dS K,  dK = scale * dS^T Q.
 // P and dS are rounded to the element type before the products that take
-// them, as the forward rounds P; everything else accumulates in fp32.
+// them, as the forward rounds P; everything else accumulates in fp32.  The
+// dK/dV kernel forms dS from the rounded P its dV product takes, the dQ
+// kernel from the unrounded P (both within one rounding of each other).
 //
 // Three kernels, all deterministic (no atomics: every gradient element is
 // summed by one wave in a fixed order):
-//   * fa_bwd_stats_kernel: per query row lse * log2(e) and rowsum(dO o O),
+//   * fa_bwd_stats_kernel: per query row lse * log2(e) and -rowsum(dO o O),
 //     into the workspace in 64-row records (one direct load per tile).
-//   * fa_bwd_dkdv_kernel: one workgroup per (batch, KV head, 128 keys), wave
-//     w owning keys k0 + 32w .. +32 with their K and V rows resident in
-//     registers.  It streams 64-row tiles of Q and dO (and their stats and
-//     mask words) through triple-buffered LDS for every query head of the
-//     group, so the GQA sum over the group happens in the accumulators;
-//     hand-ordered software pipeline, one workgroup per CU.
+//   * fa_bwd_dkdv_kernel: one workgroup of 8 waves per (batch, KV head, 128
+//     keys); waves w and w+4 own keys k0 + 32w .. +32 and split the four
+//     products (w: S, P, dV with the K rows resident; w+4: dP, dS, dK with
+//     the V rows resident, P handed over through LDS).  It streams 64-row
+//     tiles of Q and dO (and their stats and mask words) through triple-
+//     buffered LDS for every query head of the group, so the GQA sum over
+//     the group happens in the accumulators; one workgroup per CU, two waves
+//     per SIMD.
 //   * fa_bwd_dq_kernel: one workgroup per (batch, query head, 128 rows), the
 //     forward's shape: Q and dO rows resident, K and V tiles streamed through
 //     double-buffered LDS; two workgroups per CU.
@@ -104,7 +108,7 @@ __device__ __forceinline__ void put_pair(uint4v (&ops)[NOPS], int t, int i, floa
   ops[2 * t + (i >> 3)][(i & 7) >> 1] = __builtin_bit_cast(unsigned, E::pack(x, y));
 }
 
-// ---- stats: lse * log2(e) and rowsum(dO o O) per query row -----------------
+// ---- stats: lse * log2(e) and -rowsum(dO o O) per query row ----------------
 // One workgroup per (b, query head, 64-row tile); wave w takes rows 16w..16w+15,
 // D/8 lanes per row (16 bytes each).
 template <int D, bool BF16>
@@ -141,25 +145,11 @@ __global__ void __launch_bounds__(256) fa_bwd_stats_kernel(const BwdArgs a) {
         l2 = (l == -__builtin_inff()) ? __builtin_inff() : l * 1.4426950408889634f;
       }
       out[r] = l2;
-      out[kBwdStatsTile + r] = row < a.n ? acc : 0.0f;
+      out[kBwdStatsTile + r] = row < a.n ? -acc : 0.0f;
     }
   }
 }
 
-// ---- dK, dV ------------------------------------------------------------------
-// Step s of a workgroup: query head hkv * group + s % group, query tile
-// qtiles - 1 - s / group, down to qt_begin (causal: the first tile with a
-// query that sees one of the block's keys), two 32-query sub-tiles each.
-//
-// One wave per SIMD (128 accumulator, 64 operand VGPRs per lane; 123 KiB of
-// LDS), so the wave has to hide its own latencies: the loop is software
-// pipelined and hand ordered, as the forward's.  Phase (s, t) issues, one
-// MFMA per slot, the S and dP products of the *next* sub-tile, then the dV
-// and dK products of sub-tile (s, t); the softmax of (s, t) -- exp, dS, the
-// packing into B operands -- is spread over the first slots, and every LDS
-// operand read runs a few MFMAs ahead of its use.  Q/dO tiles (and their
-// stats) are triple buffered: the barrier between the two phases of step s
-// releases the buffer of step s-1, which then receives step s+2.
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 // 4-byte direct load of one lane (lane l writes dst + 4 l).
@@ -167,36 +157,49 @@ __device__ __forceinline__ void direct_load4(__amdgpu_buffer_rsrc_t r, lds_void*
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 4, voff, 0, 0, 0);
 }
 
-// MASK: an explicit mask (fa_fwd_params bit rows) hides keys too; each
-// step also stages, per wave, the 32-bit word of every query row of the tile
-// that holds the wave's 32 keys (1 KB per stage).
+// ---- dK, dV with two waves per key group -----------------------------------
+// One workgroup of 8 waves per (batch, KV head, 128 keys).  Waves w and w+4
+// (w = 0..3) own keys k0 + 32w .. +32, one key per lane, and run on the same
+// SIMD; they split each step's four products by role:
+//   * P-wave (w): S = Q K^T, P = exp2(S c2 - lse2), dV^T += dO^T P;
+//   * dS-wave (w+4): dP = dO V^T, dS = P o (dP - delta), dK^T += Q^T dS,
+// taking P from the P-wave through LDS (the 16-bit values its dV product
+// uses, 2 KB per 32-query sub-tile).  Each wave then holds one resident
+// operand (K or V rows) and one accumulator (dV or dK): at most 256 registers,
+// so two waves share each SIMD and cover each other's latencies, and every
+// MFMA accumulates in VGPRs.
+// Periods: in period p the P-waves work on step p and the dS-waves on step
+// p - 1, whose P was written in period p - 1 (exchange buffers alternate by
+// step parity).  Q/dO tiles (and their stats and mask words) are triple
+// buffered: period p reads stages p and p - 1 and loads step p + 1 into the
+// third; one barrier ends each period.
 template <int D, bool CAUSAL, bool MASK, bool BF16>
-__global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
+__global__ void __launch_bounds__(512, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
   using L = Lds<D>;
   using E = Elem<BF16>;
   constexpr int KK = D / 16;
   constexpr int MT = D / 32;
   constexpr int SEGQ = L::Segs / 4;
-  constexpr int NSD = 2 * KK;  // S and dP MFMAs of a sub-tile
-  constexpr int NGR = 4 * MT;  // dV and dK MFMAs of a sub-tile
-  constexpr int PFR = 3;       // row-operand reads run this many MFMAs ahead
-  constexpr int PFT = 2;       // transposing reads run this many MFMAs ahead
+  constexpr int PFR = 3;  // row-operand reads run this many MFMAs ahead
+  constexpr int PFT = 3;  // transposing reads run this many MFMAs ahead
   __shared__ __attribute__((aligned(1024))) _Float16 q_lds0[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 q_lds1[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 q_lds2[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 d_lds0[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 d_lds1[L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 d_lds2[L::Tile];
-  // 128 floats of stats per tile; a whole-wave direct load writes 1 KB.
   __shared__ __attribute__((aligned(1024))) float s_lds0[256];
   __shared__ __attribute__((aligned(1024))) float s_lds1[256];
   __shared__ __attribute__((aligned(1024))) float s_lds2[256];
-  // MASK: word (wave w, row r) at w * 64 + r.
   __shared__ __attribute__((aligned(1024))) uint32_t m_lds0[MASK ? 256 : 1];
   __shared__ __attribute__((aligned(1024))) uint32_t m_lds1[MASK ? 256 : 1];
   __shared__ __attribute__((aligned(1024))) uint32_t m_lds2[MASK ? 256 : 1];
+  // P exchange: [step parity][key group][sub-tile][16-query half][lane].
+  __shared__ __attribute__((aligned(1024))) uint4v x_lds[2 * 4 * 2 * 2 * 64];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int role = wave >> 2;  // 0: P-wave, 1: dS-wave
+  const int kq = wave & 3;     // key group
   const int lane = (int)threadIdx.x & 63;
   const int hi = lane >> 5, ql = lane & 31;
 
@@ -211,39 +214,35 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
   const int hkv_count = a.hq / a.group;
   const int b = u / hkv_count, hkv = u - b * hkv_count;
   const int k0 = kb * kBwdBlockKeys;
-  const int kw = k0 + 32 * wave;  // this wave's first key
-  const int krow = kw + ql;       // this lane's key
+  const int kw = k0 + 32 * kq;  // this wave's first key
+  const int krow = kw + ql;     // this lane's key
   const int N = a.n, NK = a.nk;
 
-  // K and V rows of the lane's key as B operands (n = key, k = dims).
-  half8 kf[KK], vf[KK];
+  // The wave's resident B operand: K rows (P-wave) or V rows (dS-wave) of
+  // the lane's key (n = key, k = dims).
+  half8 of[KK];
   if (krow < NK) {
-    const _Float16* kp = a.k + b * a.ksb + hkv * a.ksh + (int64_t)krow * a.ksn + 8 * hi;
-    const _Float16* vp = a.v + b * a.vsb + hkv * a.vsh + (int64_t)krow * a.vsn + 8 * hi;
+    const _Float16* src = role == 0
+        ? a.k + b * a.ksb + hkv * a.ksh + (int64_t)krow * a.ksn + 8 * hi
+        : a.v + b * a.vsb + hkv * a.vsh + (int64_t)krow * a.vsn + 8 * hi;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      kf[kk] = *(const half8*)(kp + 16 * kk);
-      vf[kk] = *(const half8*)(vp + 16 * kk);
-    }
+    for (int kk = 0; kk < KK; ++kk) of[kk] = *(const half8*)(src + 16 * kk);
   } else {
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) kf[kk] = vf[kk] = (half8)(_Float16)0;
+    for (int kk = 0; kk < KK; ++kk) of[kk] = (half8)(_Float16)0;
   }
-  float16v dk[MT], dv[MT];
+  float16v acc[MT];  // dV^T (P-wave) or dK^T (dS-wave): m = dims, n = key
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) dk[mt] = dv[mt] = (float16v)0.0f;
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = (float16v)0.0f;
 
   const int qt_begin = CAUSAL ? min(a.qtiles, max(0, k0 - a.diag) / kBwdStatsTile) : 0;
   const int per_head = a.qtiles - qt_begin;
   const int steps = a.group * per_head;
 
-  int goff_q[SEGQ], goff_d[SEGQ];
+  // P-waves load the Q tile, dS-waves the dO tile (segments kq, kq+4, ..).
+  int goff[SEGQ];
 #pragma unroll
-  for (int s = 0; s < SEGQ; ++s) {
-    goff_q[s] = seg_offset<D>(wave + 4 * s, lane, a.qsn);
-    goff_d[s] = seg_offset<D>(wave + 4 * s, lane, a.dosn);
-  }
-  // Buffers by compile-time stage index.
+  for (int s = 0; s < SEGQ; ++s) goff[s] = seg_offset<D>(kq + 4 * s, lane, role == 0 ? a.qsn : a.dosn);
   auto qbuf = [&](auto st) -> _Float16* {
     constexpr int S = decltype(st)::value % 3;
     if constexpr (S == 0) return q_lds0;
@@ -268,36 +267,31 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
     else if constexpr (S == 1) return m_lds1;
     else return m_lds2;
   };
-  // Step s takes query tile qtiles - 1 - s / group of query head s % group:
-  // tiles in descending order, every head of the group at each tile.  The
-  // key blocks running at once on an XCD (one KV head each) then all start
-  // at the last tile and walk down together, each stopping at its causal
-  // start, so they stream the same Q and dO tiles through the XCD's L2
-  // (measured +1% on the C4 training shape against head-major ascending).
-  auto qbase_of = [&](int s) {
-    const int j = s / a.group;
-    return (a.qtiles - 1 - j) * kBwdStatsTile;
+  // Steps go through the query tiles in descending order, every head of the
+  // group at each tile: a cursor (qt, h) names query tile qt of query head
+  // hkv * group + h.
+  struct Cursor {
+    int qt, h;
   };
-  // Direct loads of step s's Q and dO tiles (wave w: segments w, w+4, ..)
-  // and, by wave 0, its stats record, into the buffers of stage ST.
-  auto issue = [&](int s, auto st) {
-    _Float16* const qdst = qbuf(st);
-    _Float16* const ddst = dbuf(st);
-    const int j = s / a.group;
-    const int h = s - j * a.group;
-    const int qt = a.qtiles - 1 - j;
-    const int hq = hkv * a.group + h;
+  auto advance = [&](Cursor& c) {
+    if (++c.h == a.group) {
+      c.h = 0;
+      --c.qt;
+    }
+  };
+  auto issue = [&](const Cursor& c, auto st) {
+    const int qt = c.qt;
+    const int hq = hkv * a.group + c.h;
     const int q0 = qt * kBwdStatsTile;
     const int rows = N - q0;
-    const __amdgpu_buffer_rsrc_t rq =
-        make_rsrc(a.q + b * a.qsb + hq * a.qsh + (int64_t)q0 * a.qsn, (int)(rows * a.qsn * 2));
-    const __amdgpu_buffer_rsrc_t rd = make_rsrc(
-        a.dout + b * a.dosb + hq * a.dosh + (int64_t)q0 * a.dosn, (int)(rows * a.dosn * 2));
+    const __amdgpu_buffer_rsrc_t r = role == 0
+        ? make_rsrc(a.q + b * a.qsb + hq * a.qsh + (int64_t)q0 * a.qsn, (int)(rows * a.qsn * 2))
+        : make_rsrc(a.dout + b * a.dosb + hq * a.dosh + (int64_t)q0 * a.dosn,
+                    (int)(rows * a.dosn * 2));
+    _Float16* const dst = role == 0 ? qbuf(st) : dbuf(st);
 #pragma unroll
-    for (int s2 = 0; s2 < SEGQ; ++s2) {
-      direct_load16(rq, (lds_void*)(qdst + (wave + 4 * s2) * 512), goff_q[s2]);
-      direct_load16(rd, (lds_void*)(ddst + (wave + 4 * s2) * 512), goff_d[s2]);
-    }
+    for (int s2 = 0; s2 < SEGQ; ++s2)
+      direct_load16(r, (lds_void*)(dst + (kq + 4 * s2) * 512), goff[s2]);
     if (wave == 0) {
       const __amdgpu_buffer_rsrc_t rs = make_rsrc(
           a.stats + ((int64_t)(b * a.hq + hq) * a.qtiles + qt) * (2 * kBwdStatsTile),
@@ -305,40 +299,38 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
       direct_load16(rs, (lds_void*)sbuf(st), 16 * lane);
     }
     if constexpr (MASK) {
-      // Lane l: row q0 + l, 32-bit word 2 (k0 / 64) + wave of it; the window
-      // ends after the last row's words (rows past it and words past the
-      // keys read as 0).  Offsets of rows below N fit 32 bits (the C ABI
-      // checks N * row stride); a lane past N whose offset wraps reads 0 or
-      // some mask word inside the window, for a row that is never used.
-      const uint64_t* mrow = a.mbits + b * a.msb + hq * a.msh + (int64_t)q0 * a.msq;
-      const __amdgpu_buffer_rsrc_t rm =
-          make_rsrc(mrow, (int)((((int64_t)rows - 1) * a.msq + a.mwords) * 8));
-      direct_load4(rm, (lds_void*)(mbuf(st) + 64 * wave),
-                   (int)(lane * a.msq * 8) + (k0 / 64) * 8 + 4 * wave);
+      if (role == 0) {
+        // Lane l: row q0 + l, 32-bit word 2 (k0 / 64) + kq of it; the window
+        // ends after the last row's words (rows past it and words past the
+        // keys read as 0).  Offsets of rows below N fit 32 bits (the C ABI
+        // checks N * row stride); a lane past N whose offset wraps reads 0 or
+        // some mask word inside the window, for a row that is never used.
+        const uint64_t* mrow = a.mbits + b * a.msb + hq * a.msh + (int64_t)q0 * a.msq;
+        const __amdgpu_buffer_rsrc_t rm =
+            make_rsrc(mrow, (int)((((int64_t)rows - 1) * a.msq + a.mwords) * 8));
+        direct_load4(rm, (lds_void*)(mbuf(st) + 64 * kq),
+                     (int)(lane * a.msq * 8) + (k0 / 64) * 8 + 4 * kq);
+      }
     }
   };
 
   const TileReader<D> rd(lane);
-  // P = exp2(S c2 - lse2); c2 keeps its sign away from 0 (scale 0: uniform
-  // weights), so a score set to mval gives P = 0 exactly.
   const float c2 = a.c2 != 0.0f ? a.c2 : 1e-30f;
   const float mval = c2 > 0.0f ? -__builtin_inff() : __builtin_inff();
-  // Scores of sub-tile t of step s (stage ST) whose key is past the causal
-  // diagonal of their query (element i: query q0 + 8(i/4) + 4hi + i%4) or
-  // hidden by the mask -> mval.
-  auto mask_scores = [&](float16v sv, int s, int t, auto st)
-                         __attribute__((always_inline)) -> float16v {
+  // Scores of sub-tile t (element i: query q0 + 32t + 8(i/4) + 4hi + i%4)
+  // whose key is past the query's causal diagonal or hidden by the mask -> mval.
+  auto mask_scores = [&](float16v sv, int q0, int t, auto st) __attribute__((always_inline)) -> float16v {
     if constexpr (CAUSAL) {
-      const int q0 = qbase_of(s) + 32 * t;
-      if (kw + 31 > q0 + a.diag) {
+      const int qs = q0 + 32 * t;
+      if (kw + 31 > qs + a.diag) {
         static_for<16>([&](auto i_c) {
           constexpr int i = decltype(i_c)::value;
-          if (krow > q0 + 8 * (i >> 2) + 4 * hi + (i & 3) + a.diag) sv[i] = mval;
+          if (krow > qs + 8 * (i >> 2) + 4 * hi + (i & 3) + a.diag) sv[i] = mval;
         });
       }
     }
     if constexpr (MASK) {
-      const uint32_t* mw = mbuf(st) + 64 * wave + 32 * t + 4 * hi;
+      const uint32_t* mw = mbuf(st) + 64 * kq + 32 * t + 4 * hi;
       static_for<4>([&](auto g_c) {
         constexpr int g = decltype(g_c)::value;
         const uint4v m4 = *(const uint4v*)(mw + 8 * g);
@@ -350,175 +342,232 @@ __global__ void __launch_bounds__(256, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
     }
     return sv;
   };
+  auto xslot = [&](int par, int t, int h) -> uint4v* {
+    return x_lds + (((par * 4 + kq) * 2 + t) * 2 + h) * 64 + lane;
+  };
 
-  // S and dP of the current (index t) and next (1 - t) sub-tile.
-  float16v sb[2], db[2];
+  // Slots of one step, for either role: S (or dP) of sub-tile 0 in slots
+  // [0, KK), of sub-tile 1 in [KK, 2KK), then dV (or dK) of sub-tile 0 in
+  // [2KK, 2KK + 2MT) and of sub-tile 1 after.  The element work of sub-tile
+  // t (P, or dS) sits in the slots of the products before its consumer:
+  // sub-tile 0 in [KK, 2KK), sub-tile 1 in [2KK, 2KK + 2MT).
+  constexpr int NS = 2 * KK;
+  constexpr int NG = 2 * MT;
+  constexpr int NSLOT = NS + 2 * NG;
+  // pair pr (0..7) of sub-tile t goes to this slot.
+  constexpr auto pair_slot = [](int t, int pr) constexpr {
+    return t == 0 ? KK + (pr * KK) / 8 : NS + (pr * NG) / 8;
+  };
 
-  // Phase (s, T) on the buffers of stage B: HAS_NEXT -- the next sub-tile
-  // ((s, 1) or (s+1, 0), stage B or B+1) exists and its S, dP are computed.
-  auto phase = [&](int s, auto t_c, auto b_c, auto has_next_c) {
-    constexpr int T = decltype(t_c)::value;
-    constexpr int B = decltype(b_c)::value;
-    constexpr bool HAS_NEXT = decltype(has_next_c)::value;
-    constexpr int BN = T == 0 ? B : B + 1;  // stage of the next sub-tile
-    constexpr int TN = 1 - T;
-    constexpr int NS = HAS_NEXT ? NSD : 0;  // S/dP slots
-    constexpr int NBS = NS + NGR;           // slots
-    const _Float16* qc = qbuf(b_c);
-    const _Float16* dc = dbuf(b_c);
-    const float* sc = sbuf(b_c);
-    const _Float16* qn = qbuf(std::integral_constant<int, BN>{});
-    const _Float16* dn = dbuf(std::integral_constant<int, BN>{});
-
-    // Row statistics of this sub-tile's rows 32T + 8g + 4hi + 0..3, read a
-    // couple of slots before the first pair that needs them.
-    float4v l4[4], d4[4];
-    auto read_stats = [&](auto g_c) {
-      constexpr int g = decltype(g_c)::value;
-      l4[g] = *(const float4v*)(sc + 32 * T + 8 * g + 4 * hi);
-      d4[g] = *(const float4v*)(sc + kBwdStatsTile + 32 * T + 8 * g + 4 * hi);
-    };
-    uint4v pp[2], pd[2];  // P and dS as B operands of the two 16-query steps
-    half8 rf[NSD > 0 ? NSD : 1], tf[NGR];
-    // Row operand i of the next sub-tile: Q (even i) or dO (odd i), dims 16(i/2)..
-    auto read_row = [&](int i) -> half8 {
-      return rd.row((i & 1) ? dn : qn, TN, i >> 1);
-    };
-    // Transposed operand v: 16-query step h2 = v / (2 MT), output tile
-    // mt = (v / 2) % MT, dO^T (even v, for dV) or Q^T (odd v, for dK).
+  // P-wave, step s on stage ST, exchange parity par.
+  auto work_p = [&](const Cursor& c, auto st, int par) {
+    const _Float16* qc = qbuf(st);
+    const _Float16* dc = dbuf(st);
+    const float* sc = sbuf(st);
+    const int q0 = c.qt * kBwdStatsTile;
+    float16v sv[2];
+    float4v l4[2][4];
+    uint4v pp[2][2];
+    half8 rf[NS], tf[NG * 2];
+    auto read_row = [&](int i) -> half8 { return rd.row(qc, i / KK, i % KK); };
+    // Transposed operand v of the dV products: sub-tile v / NG, 16-query step
+    // (v % NG) / MT, output tile v % MT.
     auto read_tr = [&](int v) -> half8 {
-      return rd.tr((v & 1) ? qc : dc, 2 * T + v / (2 * MT), (v >> 1) % MT);
+      const int t = v / NG, w = v % NG;
+      return rd.tr(dc, 2 * t + w / MT, w % MT);
     };
-    auto softmax_pair = [&](auto p_c) {
-      constexpr int pr = decltype(p_c)::value;
-      constexpr int i = 2 * pr, g = i >> 2, e = i & 3;
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sb[T][i], c2, -l4[g][e]));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sb[T][i + 1], c2, -l4[g][e + 1]));
-      const float s0 = p0 * (db[T][i] - d4[g][e]);
-      const float s1 = p1 * (db[T][i + 1] - d4[g][e + 1]);
-      pp[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, E::pack(p0, p1));
-      pd[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, E::pack(s0, s1));
-    };
-    // Pair pr feeds 16-query step pr / 4, whose first MFMA is in slot
-    // NS + (pr / 4) 2 MT; within a slot the MFMA goes first, so the pair must
-    // sit in an earlier slot (-1: before the slots).  Spread from slot 1 (the
-    // statistics reads land meanwhile).
-    constexpr auto pair_slot = [](int pr) constexpr {
-      const int spread = 1 + (pr * (NS + 2 * MT - 1)) / 8;
-      const int last_ok = NS + (pr / 4) * 2 * MT - 1;
-      return spread < last_ok ? spread : last_ok;
-    };
-    // Statistics group g (pairs 2g, 2g+1) is read at stats_slot(g).
-    constexpr auto stats_slot = [pair_slot](int g) constexpr {
-      const int s = pair_slot(2 * g) - 2;
-      return s < 0 ? -1 : s;
+    auto pair = [&](int t, int pr) {
+      const int i = 2 * pr, g = i >> 2, e = i & 3;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[t][i], c2, -l4[t][g][e]));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[t][i + 1], c2, -l4[t][g][e + 1]));
+      unsigned w = __builtin_bit_cast(unsigned, E::pack(p0, p1));
+      asm volatile("" : "+v"(w));  // keeps the pair in its slot (not sunk to its use)
+      pp[t][i >> 3][(i & 7) >> 1] = w;
     };
     static_for<4>([&](auto g_c) {
-      if constexpr (stats_slot(decltype(g_c)::value) < 0) read_stats(g_c);
+      constexpr int g = decltype(g_c)::value;
+      l4[0][g] = *(const float4v*)(sc + 8 * g + 4 * hi);
     });
-    static_for<8>([&](auto p_c) {
-      if constexpr (pair_slot(decltype(p_c)::value) < 0) softmax_pair(p_c);
-    });
-    static_for<(PFR < NS ? PFR : NS)>([&](auto i_c) {
-      rf[decltype(i_c)::value] = read_row(decltype(i_c)::value);
-    });
-    static_for<NBS>([&](auto slot_c) {
+    static_for<PFR>([&](auto i_c) { rf[decltype(i_c)::value] = read_row(decltype(i_c)::value); });
+    static_for<NSLOT>([&](auto slot_c) {
       constexpr int slot = decltype(slot_c)::value;
-      if constexpr (slot == (NS >= PFT ? NS - PFT : 0)) {
+      if constexpr (slot == NS - PFT) {
         static_for<PFT>([&](auto v_c) { tf[decltype(v_c)::value] = read_tr(decltype(v_c)::value); });
       }
-      if constexpr (slot >= NS && slot - NS + PFT < NGR) tf[slot - NS + PFT] = read_tr(slot - NS + PFT);
+      if constexpr (slot >= NS && slot - NS + PFT < 2 * NG) tf[slot - NS + PFT] = read_tr(slot - NS + PFT);
       if constexpr (slot < NS) {
-        constexpr int i = slot, kk = i >> 1;
-        if constexpr (i + PFR < NS) rf[i + PFR] = read_row(i + PFR);
-        if constexpr ((i & 1) == 0)
-          sb[TN] = E::mfma(rf[i], kf[kk], kk == 0 ? (float16v)0.0f : sb[TN]);
-        else
-          db[TN] = E::mfma(rf[i], vf[kk], kk == 0 ? (float16v)0.0f : db[TN]);
+        constexpr int t = slot / KK, kk = slot % KK;
+        if constexpr (slot + PFR < NS) rf[slot + PFR] = read_row(slot + PFR);
+        sv[t] = E::mfma(rf[slot], of[kk], kk == 0 ? (float16v)0.0f : sv[t]);
       } else {
-        constexpr int v = slot - NS, h2 = v / (2 * MT), mt = (v >> 1) % MT;
-        if constexpr ((v & 1) == 0)
-          dv[mt] = E::mfma(tf[v], __builtin_bit_cast(half8, pp[h2]), dv[mt]);
-        else
-          dk[mt] = E::mfma(tf[v], __builtin_bit_cast(half8, pd[h2]), dk[mt]);
+        constexpr int v = slot - NS, t = v / NG, w = v % NG, h2 = w / MT, mt = w % MT;
+        acc[mt] = E::mfma(tf[v], __builtin_bit_cast(half8, pp[t][h2]), acc[mt]);
       }
-      static_for<4>([&](auto g_c) {
-        if constexpr (stats_slot(decltype(g_c)::value) == slot) read_stats(g_c);
-      });
+      fence_schedule();  // the slot's MFMA issues before its element work
+      if constexpr (slot == KK) {
+        static_for<4>([&](auto g_c) {
+          constexpr int g = decltype(g_c)::value;
+          l4[1][g] = *(const float4v*)(sc + 32 + 8 * g + 4 * hi);
+        });
+        sv[0] = mask_scores(sv[0], q0, 0, st);
+      }
+      if constexpr (slot == NS) sv[1] = mask_scores(sv[1], q0, 1, st);
       static_for<8>([&](auto p_c) {
-        if constexpr (pair_slot(decltype(p_c)::value) == slot) softmax_pair(p_c);
+        constexpr int pr = decltype(p_c)::value;
+        if constexpr (pair_slot(0, pr) == slot) pair(0, pr);
+        if constexpr (pair_slot(1, pr) == slot) pair(1, pr);
+      });
+      if constexpr (slot == NS) {
+        *xslot(par, 0, 0) = pp[0][0];
+        *xslot(par, 0, 1) = pp[0][1];
+      }
+      if constexpr (slot == NS + NG) {
+        *xslot(par, 1, 0) = pp[1][0];
+        *xslot(par, 1, 1) = pp[1][1];
+      }
+      fence_schedule();
+    });
+  };
+
+  // dS-wave, one step on stage ST with exchange parity par.  The dP products
+  // accumulate onto -delta (the stats record holds -rowsum(dO o O)), so
+  // dS = P (dP - delta) is one multiply per element.
+  auto work_ds = [&](auto st, int par) {
+    const _Float16* qc = qbuf(st);
+    const _Float16* dc = dbuf(st);
+    const float* sc = sbuf(st);
+    float16v dp[2];
+    float16v nd[2];
+    uint4v pr2[2][2], pd[2][2];
+    half8 rf[NS], tf[NG * 2];
+    auto read_row = [&](int i) -> half8 { return rd.row(dc, i / KK, i % KK); };
+    auto read_tr = [&](int v) -> half8 {
+      const int t = v / NG, w = v % NG;
+      return rd.tr(qc, 2 * t + w / MT, w % MT);
+    };
+    auto read_nd = [&](int t) {
+      static_for<4>([&](auto g_c) {
+        constexpr int g = decltype(g_c)::value;
+        const float4v v = *(const float4v*)(sc + kBwdStatsTile + 32 * t + 8 * g + 4 * hi);
+        nd[t][4 * g + 0] = v[0];
+        nd[t][4 * g + 1] = v[1];
+        nd[t][4 * g + 2] = v[2];
+        nd[t][4 * g + 3] = v[3];
+      });
+    };
+    auto pair = [&](int t, int pr) {
+      const int i = 2 * pr;
+      const unsigned w = pr2[t][i >> 3][(i & 7) >> 1];
+      unsigned w2 = __builtin_bit_cast(unsigned, E::pack(E::mul_lo(w, dp[t][i]), E::mul_hi(w, dp[t][i + 1])));
+      asm volatile("" : "+v"(w2));  // keeps the pair in its slot
+      pd[t][i >> 3][(i & 7) >> 1] = w2;
+    };
+    read_nd(0);
+    static_for<PFR>([&](auto i_c) { rf[decltype(i_c)::value] = read_row(decltype(i_c)::value); });
+    static_for<NSLOT>([&](auto slot_c) {
+      constexpr int slot = decltype(slot_c)::value;
+      if constexpr (slot == NS - PFT) {
+        static_for<PFT>([&](auto v_c) { tf[decltype(v_c)::value] = read_tr(decltype(v_c)::value); });
+      }
+      if constexpr (slot >= NS && slot - NS + PFT < 2 * NG) tf[slot - NS + PFT] = read_tr(slot - NS + PFT);
+      if constexpr (slot < NS) {
+        constexpr int t = slot / KK, kk = slot % KK;
+        if constexpr (slot + PFR < NS) rf[slot + PFR] = read_row(slot + PFR);
+        dp[t] = E::mfma(rf[slot], of[kk], kk == 0 ? nd[t] : dp[t]);
+      } else {
+        constexpr int v = slot - NS, t = v / NG, w = v % NG, h2 = w / MT, mt = w % MT;
+        acc[mt] = E::mfma(tf[v], __builtin_bit_cast(half8, pd[t][h2]), acc[mt]);
+      }
+      fence_schedule();
+      if constexpr (slot == 1) {
+        pr2[0][0] = *xslot(par, 0, 0);
+        pr2[0][1] = *xslot(par, 0, 1);
+      }
+      if constexpr (slot == 2) read_nd(1);
+      if constexpr (slot == KK) {
+        pr2[1][0] = *xslot(par, 1, 0);
+        pr2[1][1] = *xslot(par, 1, 1);
+      }
+      static_for<8>([&](auto p_c) {
+        constexpr int pr = decltype(p_c)::value;
+        if constexpr (pair_slot(0, pr) == slot) pair(0, pr);
+        if constexpr (pair_slot(1, pr) == slot) pair(1, pr);
       });
       fence_schedule();
     });
-    if constexpr (HAS_NEXT)
-      sb[TN] = mask_scores(sb[TN], T == 0 ? s : s + 1, TN, std::integral_constant<int, BN>{});
-  };
-
-  // Step s on stage B; LAST: no step s+1.
-  auto step = [&](int s, auto b_c, auto last_c) {
-    constexpr int B = decltype(b_c)::value;
-    constexpr bool LAST = decltype(last_c)::value;
-    phase(s, std::integral_constant<int, 0>{}, b_c, Flag<true>{});
-    // Step s+1's tiles have landed, and every wave is past its last read of
-    // stage B+2 (step s-1), which now receives step s+2.
-    barrier_after_loads<0>();
-    if (s + 2 < steps) issue(s + 2, std::integral_constant<int, B + 2>{});
-    phase(s, std::integral_constant<int, 1>{}, b_c, Flag<!LAST>{});
   };
 
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
+  // Period p loads step p + 1 into stage (p + 1) % 3 and ends with the barrier
+  // that publishes it (and the P of step p); the roles run separate loops
+  // with the same number of barriers.
   if (steps > 0) {
-    issue(0, I0{});
-    if (steps > 1) {
-      issue(1, I1{});
-      barrier_after_loads<2 * SEGQ>();  // step 0's loads (wave 0: and one of step 1's)
+    Cursor ic{a.qtiles - 1, 0};  // next step to load
+    Cursor wc{a.qtiles - 1, 0};  // step to work on
+    issue(ic, I0{});
+    advance(ic);
+    barrier_after_loads<0>();
+    if (role == 0) {
+      // Period p: step p.
+      for (int p = 0; p < steps; ++p) {
+        auto body = [&](auto st_c) {
+          constexpr int ST = decltype(st_c)::value;
+          if (p + 1 < steps) {
+            issue(ic, std::integral_constant<int, ST + 1>{});
+            advance(ic);
+          }
+          work_p(wc, st_c, p & 1);
+          advance(wc);
+          barrier_after_loads<0>();
+        };
+        const int m3 = p % 3;
+        if (m3 == 0) body(I0{});
+        else if (m3 == 1) body(I1{});
+        else body(I2{});
+      }
     } else {
+      // Period p: step p - 1; period `steps` has no barrier after it.
+      if (1 < steps) {
+        issue(ic, I1{});
+        advance(ic);
+      }
       barrier_after_loads<0>();
-    }
-    // S and dP of sub-tile (0, 0).
-    sb[0] = db[0] = (float16v)0.0f;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      sb[0] = E::mfma(rd.row(q_lds0, 0, kk), kf[kk], sb[0]);
-      db[0] = E::mfma(rd.row(d_lds0, 0, kk), vf[kk], db[0]);
-    }
-    sb[0] = mask_scores(sb[0], 0, 0, I0{});
-    int s = 0;
-    for (; s + 3 < steps; s += 3) {
-      step(s, I0{}, Flag<false>{});
-      step(s + 1, I1{}, Flag<false>{});
-      step(s + 2, I2{}, Flag<false>{});
-    }
-    const int rest = steps - s;  // 1..3
-    if (rest == 1) {
-      step(s, I0{}, Flag<true>{});
-    } else if (rest == 2) {
-      step(s, I0{}, Flag<false>{});
-      step(s + 1, I1{}, Flag<true>{});
-    } else {
-      step(s, I0{}, Flag<false>{});
-      step(s + 1, I1{}, Flag<false>{});
-      step(s + 2, I2{}, Flag<true>{});
+      for (int p = 1; p < steps; ++p) {
+        auto body = [&](auto st_c) {
+          constexpr int ST = decltype(st_c)::value;
+          if (p + 1 < steps) {
+            issue(ic, std::integral_constant<int, ST + 1>{});
+            advance(ic);
+          }
+          work_ds(std::integral_constant<int, ST + 2>{}, (p - 1) & 1);
+          barrier_after_loads<0>();
+        };
+        const int m3 = p % 3;
+        if (m3 == 0) body(I0{});
+        else if (m3 == 1) body(I1{});
+        else body(I2{});
+      }
+      const int m3 = (steps - 1) % 3;
+      if (m3 == 0) work_ds(I0{}, (steps - 1) & 1);
+      else if (m3 == 1) work_ds(I1{}, (steps - 1) & 1);
+      else work_ds(I2{}, (steps - 1) & 1);
     }
   }
 
   if (krow < NK) {
-    _Float16* dkp = a.dk + b * a.dksb + hkv * a.dksh + (int64_t)krow * a.dksn;
-    _Float16* dvp = a.dv + b * a.dvsb + hkv * a.dvsh + (int64_t)krow * a.dvsn;
+    _Float16* dst = role == 0 ? a.dv + b * a.dvsb + hkv * a.dvsh + (int64_t)krow * a.dvsn
+                              : a.dk + b * a.dksb + hkv * a.dksh + (int64_t)krow * a.dksn;
+    const float f = role == 0 ? 1.0f : a.scale;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        half4 vk, vv;
+        half4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vk[e] = E::round(dk[mt][4 * g + e] * a.scale);
-          vv[e] = E::round(dv[mt][4 * g + e]);
-        }
-        *(half4*)(dkp + 32 * mt + 8 * g + 4 * hi) = vk;
-        *(half4*)(dvp + 32 * mt + 8 * g + 4 * hi) = vv;
+        for (int e = 0; e < 4; ++e) v[e] = E::round(acc[mt][4 * g + e] * f);
+        *(half4*)(dst + 32 * mt + 8 * g + 4 * hi) = v;
       }
     }
   }
@@ -557,7 +606,7 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
 
   // Q and dO rows of the lane's query as B operands (n = query, k = dims).
   half8 qf[KK], df[KK];
-  float lse2 = __builtin_inff(), delta = 0.0f;
+  float lse2 = __builtin_inff(), ndelta = 0.0f;
   if (qrow < N) {
     const _Float16* qp = a.q + b * a.qsb + hq * a.qsh + (int64_t)qrow * a.qsn + 8 * hi;
     const _Float16* dp = a.dout + b * a.dosb + hq * a.dosh + (int64_t)qrow * a.dosn + 8 * hi;
@@ -568,7 +617,7 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
     }
     const float* st = a.stats + ((int64_t)bh * a.qtiles + qrow / kBwdStatsTile) * (2 * kBwdStatsTile);
     lse2 = st[qrow % kBwdStatsTile];
-    delta = st[kBwdStatsTile + qrow % kBwdStatsTile];
+    ndelta = st[kBwdStatsTile + qrow % kBwdStatsTile];
   } else {
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) qf[kk] = df[kk] = (half8)(_Float16)0;
@@ -637,7 +686,7 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
           if (key + 1 >= NK || (CAUSAL && key + 1 > qrow + a.diag) || ((mw >> (kt + 1)) & 1) == 0)
             p1 = 0.0f;
         }
-        put_pair<E>(pd, t, i, p0 * (dpa[i] - delta), p1 * (dpa[i + 1] - delta));
+        put_pair<E>(pd, t, i, p0 * (dpa[i] + ndelta), p1 * (dpa[i + 1] + ndelta));
       }
     }
 #pragma unroll
@@ -686,14 +735,14 @@ void launch_bwd(const BwdArgs& a, int batch, bool causal, hipStream_t stream) {
     hipLaunchKernelGGL((fa_bwd_stats_kernel<D, BF16>), dim3(stats_wgs), dim3(256), 0, stream, a);
   if (causal) {
     if (dkdv_wgs > 0)
-      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, true, MASK, BF16>), dim3(dkdv_wgs), dim3(256), 0,
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, true, MASK, BF16>), dim3(dkdv_wgs), dim3(512), 0,
                          stream, a);
     if (dq_wgs > 0)
       hipLaunchKernelGGL((fa_bwd_dq_kernel<D, true, MASK, BF16>), dim3(dq_wgs), dim3(256), 0, stream,
                          a);
   } else {
     if (dkdv_wgs > 0)
-      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, false, MASK, BF16>), dim3(dkdv_wgs), dim3(256), 0,
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, false, MASK, BF16>), dim3(dkdv_wgs), dim3(512), 0,
                          stream, a);
     if (dq_wgs > 0)
       hipLaunchKernelGGL((fa_bwd_dq_kernel<D, false, MASK, BF16>), dim3(dq_wgs), dim3(256), 0, stream,

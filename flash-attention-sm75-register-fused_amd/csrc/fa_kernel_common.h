@@ -45,6 +45,21 @@ struct Elem<false> {  // binary16
   }
   static __device__ __forceinline__ _Float16 round(float x) { return (_Float16)x; }
   static __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+  // The low and high value of a packed pair, exactly.
+  static __device__ __forceinline__ float lo_f32(unsigned w) {
+    return (float)__builtin_bit_cast(half2v, w)[0];
+  }
+  static __device__ __forceinline__ float hi_f32(unsigned w) {
+    return (float)__builtin_bit_cast(half2v, w)[1];
+  }
+  // x times the low (high) value of a packed pair, one rounding (an fma with
+  // a zero addend: one v_fma_mix_f32 that reads the 16-bit half in place).
+  static __device__ __forceinline__ float mul_lo(unsigned w, float x) {
+    return __builtin_fmaf(lo_f32(w), x, 0.0f);
+  }
+  static __device__ __forceinline__ float mul_hi(unsigned w, float x) {
+    return __builtin_fmaf(hi_f32(w), x, 0.0f);
+  }
 };
 template <>
 struct Elem<true> {  // bfloat16
@@ -65,6 +80,12 @@ struct Elem<true> {  // bfloat16
   static __device__ __forceinline__ float to_f32(_Float16 x) {
     return __builtin_bit_cast(float, (unsigned)__builtin_bit_cast(unsigned short, x) << 16);
   }
+  static __device__ __forceinline__ float lo_f32(unsigned w) { return __builtin_bit_cast(float, w << 16); }
+  static __device__ __forceinline__ float hi_f32(unsigned w) {
+    return __builtin_bit_cast(float, w & 0xffff0000u);
+  }
+  static __device__ __forceinline__ float mul_lo(unsigned w, float x) { return lo_f32(w) * x; }
+  static __device__ __forceinline__ float mul_hi(unsigned w, float x) { return hi_f32(w) * x; }
 };
 
 // -x of every element (sign flip; exact in either element type).
