@@ -510,49 +510,50 @@ __global__ void __launch_bounds__(512, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
     advance(ic);
     barrier_after_loads<0>();
     if (role == 0) {
-      // Period p: step p.
-      for (int p = 0; p < steps; ++p) {
-        auto body = [&](auto st_c) {
-          constexpr int ST = decltype(st_c)::value;
-          if (p + 1 < steps) {
-            issue(ic, std::integral_constant<int, ST + 1>{});
-            advance(ic);
-          }
-          work_p(wc, st_c, p & 1);
-          advance(wc);
-          barrier_after_loads<0>();
-        };
-        const int m3 = p % 3;
-        if (m3 == 0) body(I0{});
-        else if (m3 == 1) body(I1{});
-        else body(I2{});
+      // Period p: step p.  Unrolled by three (the stage is p % 3).
+      auto body = [&](int p, auto st_c) {
+        constexpr int ST = decltype(st_c)::value;
+        if (p + 1 < steps) {
+          issue(ic, std::integral_constant<int, ST + 1>{});
+          advance(ic);
+        }
+        work_p(wc, st_c, p & 1);
+        advance(wc);
+        barrier_after_loads<0>();
+      };
+      int p = 0;
+      for (; p + 3 <= steps; p += 3) {
+        body(p, I0{});
+        body(p + 1, I1{});
+        body(p + 2, I2{});
       }
+      if (p < steps) body(p, I0{});
+      if (p + 1 < steps) body(p + 1, I1{});
     } else {
-      // Period p: step p - 1; period `steps` has no barrier after it.
+      // Period p: step p - 1 (stage (p - 1) % 3); period `steps` has no
+      // barrier after it.  Unrolled by three from period 1.
       if (1 < steps) {
         issue(ic, I1{});
         advance(ic);
       }
       barrier_after_loads<0>();
-      for (int p = 1; p < steps; ++p) {
-        auto body = [&](auto st_c) {
-          constexpr int ST = decltype(st_c)::value;
-          if (p + 1 < steps) {
-            issue(ic, std::integral_constant<int, ST + 1>{});
-            advance(ic);
-          }
-          work_ds(std::integral_constant<int, ST + 2>{}, (p - 1) & 1);
-          barrier_after_loads<0>();
-        };
-        const int m3 = p % 3;
-        if (m3 == 0) body(I0{});
-        else if (m3 == 1) body(I1{});
-        else body(I2{});
+      auto body = [&](int p, auto st_c) {
+        constexpr int ST = decltype(st_c)::value;
+        if (p + 1 < steps) {
+          issue(ic, std::integral_constant<int, ST + 2>{});
+          advance(ic);
+        }
+        work_ds(st_c, (p - 1) & 1);
+        if (p < steps) barrier_after_loads<0>();
+      };
+      int p = 1;
+      for (; p + 2 <= steps; p += 3) {
+        body(p, I0{});
+        body(p + 1, I1{});
+        body(p + 2, I2{});
       }
-      const int m3 = (steps - 1) % 3;
-      if (m3 == 0) work_ds(I0{}, (steps - 1) & 1);
-      else if (m3 == 1) work_ds(I1{}, (steps - 1) & 1);
-      else work_ds(I2{}, (steps - 1) & 1);
+      if (p <= steps) body(p, I0{});
+      if (p + 1 <= steps) body(p + 1, I1{});
     }
   }
 
