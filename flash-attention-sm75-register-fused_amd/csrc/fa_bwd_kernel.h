@@ -627,6 +627,8 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) dq[mt] = (float16v)0.0f;
 
+  // dP accumulates onto -delta (every element of a lane is the lane's query).
+  const float16v ndv = (float16v)ndelta;
   const int kv_len = CAUSAL ? max(0, min(NK, q0 + kBwdBlockRows + a.diag)) : NK;
   const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
   // MASK: the lane's mask row (rows past N read row N - 1; not stored).
@@ -670,7 +672,7 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
     uint4v pd[4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      float16v sa = (float16v)0.0f, dpa = (float16v)0.0f;
+      float16v sa = (float16v)0.0f, dpa = ndv;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) sa = E::mfma(rd.row(kc, t, kk), qf[kk], sa);
 #pragma unroll
@@ -687,7 +689,7 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
           if (key + 1 >= NK || (CAUSAL && key + 1 > qrow + a.diag) || ((mw >> (kt + 1)) & 1) == 0)
             p1 = 0.0f;
         }
-        put_pair<E>(pd, t, i, p0 * (dpa[i] + ndelta), p1 * (dpa[i + 1] + ndelta));
+        put_pair<E>(pd, t, i, p0 * dpa[i], p1 * dpa[i + 1]);
       }
     }
 #pragma unroll

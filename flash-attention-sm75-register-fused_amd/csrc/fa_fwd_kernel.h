@@ -288,8 +288,13 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       else if constexpr (S == 1) return v_lds1 + gofs;
       else return v_lds2 + gofs;
     };
+    // The offset is recomputed at each load (an opaque SGPR): hoisted, the
+    // 4 x SEGQ segment addresses would live in SGPRs across the loop and be
+    // spilled to VGPR lanes, each reload a v_readlane in the MFMA slots.
     auto lds_seg = [&](_Float16* tile, int s) -> lds_void* {
-      return (lds_void*)(tile + (wq + 4 * s) * 512);
+      int off = (wq + 4 * s) * 512;
+      asm volatile("" : "+s"(off));
+      return (lds_void*)(tile + off);
     };
     // Buffer windows of tile j (empty past the last tile: every lane reads 0).
     auto k_window = [&](int j) {
