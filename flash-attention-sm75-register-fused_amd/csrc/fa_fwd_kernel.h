@@ -479,6 +479,11 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         const int s = first + (i * span) / 16;
         return s < NB - 1 ? s : NB - 1;
       };
+      constexpr auto last_max_slot = [max_slot]() constexpr {
+        int m = 0;
+        for (int e = 0; e < 32; ++e) m = max_slot(e) > m ? max_slot(e) : m;
+        return m;
+      };
       auto softmax_pair = [&](auto p_c) {
         constexpr int p = decltype(p_c)::value;
         constexpr int e = 2 * p;
@@ -537,6 +542,9 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
             constexpr int e = decltype(e_c)::value;
             if constexpr (max_slot(e) == slot) mx_next = fmaxf(mx_next, s_nxt[e >> 4][e & 15]);
           });
+          // Pinned after its last update: otherwise the compiler sinks the whole
+          // max chain into prepare's unmasked path, out of the MFMA slots.
+          if constexpr (slot == last_max_slot()) asm volatile("" : "+v"(mx_next));
         }
         static_for<16>([&](auto p_c) {
           if constexpr (pair_slot(decltype(p_c)::value) == slot) softmax_pair(p_c);
