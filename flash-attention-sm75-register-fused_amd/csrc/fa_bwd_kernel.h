@@ -129,10 +129,12 @@ __global__ void __launch_bounds__(256) fa_bwd_stats_kernel(const BwdArgs a) {
     const int row = qt * kBwdStatsTile + r;
     float acc = 0.0f;
     if (row < a.n) {
-      const half8 o8 =
-          *(const half8*)(a.o + b * a.osb + hq * a.osh + (int64_t)row * a.osn + 8 * part);
-      const half8 d8 =
-          *(const half8*)(a.dout + b * a.dosb + hq * a.dosh + (int64_t)row * a.dosn + 8 * part);
+      // Non-temporal loads: O is read once here (dO again by the other kernels,
+      // long after).
+      const half8 o8 = __builtin_nontemporal_load(
+          (const half8*)(a.o + b * a.osb + hq * a.osh + (int64_t)row * a.osn + 8 * part));
+      const half8 d8 = __builtin_nontemporal_load(
+          (const half8*)(a.dout + b * a.dosb + hq * a.dosh + (int64_t)row * a.dosn + 8 * part));
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(E::to_f32(o8[j]), E::to_f32(d8[j]), acc);
     }

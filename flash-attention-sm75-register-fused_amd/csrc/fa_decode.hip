@@ -187,8 +187,11 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     const int rows_left = valid ? NK - kb : 0;
     const __amdgpu_buffer_rsrc_t rv =
         make_rsrc(Vp + (int64_t)kb * a.vsn, rows_left > 0 ? rows_left * (int)a.vsn * 2 : 0);
+    // Non-temporal: every V row is read once (measured +13-17% on the
+    // long-context shapes; the K loads, 32 rows x 32 bytes per instruction,
+    // stay cached so that the other half of each line hits).
 #pragma unroll
-    for (int s = 0; s < SEGS; ++s) direct_load16(rv, (lds_void*)(tile + s * 512), goff_v[s]);
+    for (int s = 0; s < SEGS; ++s) direct_load16_nt(rv, (lds_void*)(tile + s * 512), goff_v[s]);
   };
   _Float16* const my_v0 = v_lds0 + wave * L::Tile;
   _Float16* const my_v1 = v_lds1 + wave * L::Tile;

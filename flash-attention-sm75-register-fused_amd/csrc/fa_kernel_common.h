@@ -155,6 +155,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 __device__ __forceinline__ void direct_load16(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
 }
+// The same with the non-temporal policy (the "nt" bit: streamed data that no
+// other workgroup reads again, e.g. a KV cache in decode).
+__device__ __forceinline__ void direct_load16_nt(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 2);
+}
 
 // Freezes the instruction order at this point (nothing is moved across).
 __device__ __forceinline__ void fence_schedule() { __builtin_amdgcn_sched_barrier(0); }
