@@ -4,8 +4,9 @@ No reference counterpart: the reference's backward raises
 (src/flash_attention_sm75/ops.py:47-52).  The oracle
 (attention_backward_f64, pinned in test_oracle_backward.py) is the exact
 gradient of the same fp16/bf16 inputs.  The kernels round P and dS to the
-element type before the products that take them (as the forward rounds P),
-use the rounded forward output in rowsum(dO o O), and round the gradients;
+element type before the products that take them (as the forward rounds P;
+the dK/dV kernel forms dS from that rounded P), use the rounded forward
+output in rowsum(dO o O), and round the gradients;
 each of those is a relative 2^-11 (binary16) or 2^-8 (bfloat16) error on
 terms of mixed sign.  Bar, per gradient tensor G against its oracle R:
     |G - R| <= ATOL * max|R| + RTOL * |R|   elementwise,
@@ -86,6 +87,23 @@ def test_backward_matches_oracle(device, B, Hq, Hkv, Nq, Nk, D, causal):
     grads = run_backward(q, k, v, do, causal, device)
     want = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=CODE[causal])
     assert_grads(grads, want, torch.float16, f"Nq{Nq} Nk{Nk} D{D}")
+
+
+# The dK/dV kernel runs its two roles in periods (one per step = one 64-row
+# query tile of one query head), unrolled by three with one or two periods
+# left over: these shapes give every step count from 1 to 8 and 12 for one
+# 128-key block (steps = heads per KV head x query tiles).
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hq,Hkv,Nq", [(1, 1, 64), (1, 1, 128), (1, 1, 192), (1, 1, 256),
+                                       (1, 1, 300), (3, 1, 128), (7, 7, 448), (2, 1, 256),
+                                       (4, 1, 192)])
+def test_backward_period_counts(device, Hq, Hkv, Nq, D):
+    print(f"[bwd periods] Hq={Hq} Hkv={Hkv} Nq={Nq} Nk=128 D={D}", flush=True)
+    q, k, v = seeded((1, Hq, Nq, D), 11), seeded((1, Hkv, 128, D), 12), seeded((1, Hkv, 128, D), 13)
+    do = seeded((1, Hq, Nq, D), 14)
+    grads = run_backward(q, k, v, do, False, device)
+    want = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=0)
+    assert_grads(grads, want, torch.float16, f"Hq{Hq} Nq{Nq} D{D}")
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,Nq,Nk,D,causal", [
