@@ -661,8 +661,13 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
   const TileReader<D> rd(lane);
   const float c2 = a.c2;
 
-  auto step = [&](int j, auto par_t) {
+  // One key tile j on buffer parity PAR.  MASKED: the tile may need the
+  // per-element mask (tested per pair, on this wave's need_mask); the
+  // unmasked tiles run without any mask code, so the compiler interleaves
+  // their exps with the MFMAs (a branch per pair splits the tile into blocks).
+  auto step = [&](int j, auto par_t, auto masked_t) {
     constexpr int PAR = decltype(par_t)::value;
+    constexpr bool MASKED = decltype(masked_t)::value;
     const _Float16* kc = PAR ? k_lds1 : k_lds0;
     const _Float16* vc = PAR ? v_lds1 : v_lds0;
     if (j + 1 < ntiles) issue(j + 1, PAR ? k_lds0 : k_lds1, PAR ? v_lds0 : v_lds1);
@@ -672,13 +677,6 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
     bool need_mask = kstart + kBlockN > NK || (CAUSAL && kstart + kBlockN - 1 > qw + a.diag);
     if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
     uint4v pd[4];
-    // MASKED: the tile needs the per-element mask.  At head_dim 64 without a
-    // boolean mask the two cases are separate code (the branch-free one
-    // interleaves the exps with the MFMAs: +2-5%); otherwise the second copy
-    // does not fit the registers, so the mask stays a branch per pair.
-    constexpr bool SPLIT_MASK = D == 64 && !MASK;
-    auto tile_body = [&](auto masked_c) {
-    constexpr bool MASKED = decltype(masked_c)::value;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       float16v sa = (float16v)0.0f, dpa = ndv;
@@ -691,7 +689,7 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
       for (int i = 0; i < 16; i += 2) {
         float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i], c2, -lse2));
         float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i + 1], c2, -lse2));
-        if (SPLIT_MASK ? MASKED : need_mask) {
+        if (MASKED && need_mask) {
           const int kt = 32 * t + 8 * (i >> 2) + 4 * hi + (i & 3);  // key within the tile
           const int key = kstart + kt;
           if (key >= NK || (CAUSAL && key > qrow + a.diag) || ((mw >> kt) & 1) == 0) p0 = 0.0f;
@@ -700,13 +698,6 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
         }
         put_pair<E>(pd, t, i, p0 * dpa[i], p1 * dpa[i + 1]);
       }
-    }
-    };
-    if constexpr (SPLIT_MASK) {
-      if (need_mask) tile_body(Flag<true>{});
-      else tile_body(Flag<false>{});
-    } else {
-      tile_body(Flag<true>{});
     }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -717,14 +708,29 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
     barrier_after_loads<0>();
   };
 
+  // Tiles [0, j_split) need no mask for any wave of the workgroup (wave 0,
+  // whose rows come first, is the first to meet its diagonal; every tile
+  // lies inside the keys); the rest run the masked step.  With a boolean mask
+  // any tile may need it.
+  int j_split = 0;
+  if (!MASK) {
+    j_split = min(ntiles, NK / kBlockN);
+    if (CAUSAL) j_split = min(j_split, max(0, q0 + a.diag + 1) / kBlockN);
+  }
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
   if (ntiles > 0) issue(0, k_lds0, v_lds0);
   barrier_after_loads<0>();
   int j = 0;
-  for (; j + 1 < ntiles; j += 2) {
-    step(j, std::integral_constant<int, 0>{});
-    step(j + 1, std::integral_constant<int, 1>{});
+  for (; j + 1 < j_split; j += 2) {
+    step(j, P0{}, Flag<false>{});
+    step(j + 1, P1{}, Flag<false>{});
   }
-  if (j < ntiles) step(j, std::integral_constant<int, 0>{});
+  if (j < j_split) step(j++, P0{}, Flag<false>{});
+  for (; j < ntiles; ++j) {
+    if (j & 1) step(j, P1{}, Flag<true>{});
+    else step(j, P0{}, Flag<true>{});
+  }
 
   if (qrow < N) {
     _Float16* op = a.dq + b * a.dqsb + hq * a.dqsh + (int64_t)qrow * a.dqsn;
