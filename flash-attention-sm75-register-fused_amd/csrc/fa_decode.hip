@@ -391,20 +391,24 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
 
 // Merges the splits of one (unit, query column) with 256 threads:
 // O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, M = max_s m_s.
-// The split weights are computed once (one thread per split) and kept in
-// LDS; the O sum is spread over 256 / D groups of D threads (one dimension
-// each), each taking every (256 / D)-th split with independent loads in
-// flight, and the groups' sums meet in LDS.
+// Thread (grp, dim) of the 256 / D groups of D threads takes every
+// (256 / D)-th split from grp: it loads the (max, sum) records and its
+// dimension of the partial O of four splits at a time, all independent of
+// each other, and folds them into its own running (max, sum, O) as the
+// prefill kernel folds key tiles; the groups' states merge once through
+// LDS.  One round trip to memory per four splits and one barrier: the
+// partials come from other XCDs' caches or HBM, so a merge that waits for
+// the maxima before it asks for the sums and the O values pays that latency
+// three times.
 constexpr int kCombineThreads = 256;
-constexpr int kMaxSplits = 1024;
+constexpr int kMaxSplits = 1024;  // splits per unit (the plan's bound)
 
 template <int D, bool BF16>
 __global__ void __launch_bounds__(kCombineThreads) fa_decode_combine(const DecArgs d) {
   const FwdArgs& a = d.f;
   constexpr int GROUPS = kCombineThreads / D;
-  __shared__ float w_s[kMaxSplits];
-  __shared__ float red[kCombineThreads];
-  __shared__ float o_part[GROUPS][D];
+  __shared__ float m_grp[GROUPS], l_grp[GROUPS];
+  __shared__ float o_grp[GROUPS][D];
   const int tid = threadIdx.x;
   const int unit = (int)blockIdx.x / d.rows;
   const int c = (int)blockIdx.x - unit * d.rows;  // query column of the unit
@@ -421,56 +425,64 @@ __global__ void __launch_bounds__(kCombineThreads) fa_decode_combine(const DecAr
   const int64_t p0 = (int64_t)unit * d.splits * d.rows + c;  // split s: p0 + s * rows
   const int S = d.splits;
 
-  // maximum over the splits
-  float m = -__builtin_inff();
-  for (int s = tid; s < S; s += kCombineThreads) {
-    const float ms = d.part_ml[2 * (p0 + (int64_t)s * d.rows)];
-    w_s[s] = ms;
-    m = fmaxf(m, ms);
-  }
-  red[tid] = m;
-  __syncthreads();
-  for (int off = kCombineThreads / 2; off > 0; off >>= 1) {
-    if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
-    __syncthreads();
-  }
-  const float M = red[0];
-  __syncthreads();
-  // weights and the weighted sum of l
-  float lsum = 0.0f;
-  for (int s = tid; s < S; s += kCombineThreads) {
-    const float ms = w_s[s];
-    const float w = (ms == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-    w_s[s] = w;
-    lsum += w * d.part_ml[2 * (p0 + (int64_t)s * d.rows) + 1];
-  }
-  red[tid] = lsum;
-  __syncthreads();
-  for (int off = kCombineThreads / 2; off > 0; off >>= 1) {
-    if (tid < off) red[tid] += red[tid + off];
-    __syncthreads();
-  }
-  const float Ltot = red[0];
-
-  // weighted O: group grp handles splits grp, grp + GROUPS, ...
   const int dim = tid % D;
   const int grp = tid / D;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr float kNegInf = -__builtin_inff();
+  // Running state of this thread's splits: max (log2 units), sum, O[dim]
+  // relative to that max.  A split that saw no key has max -inf and adds
+  // nothing (2^-inf = 0); while every split so far is such, the state stays
+  // (-inf, 0, 0).
+  float m_run = kNegInf, l_run = 0.0f, o_run = 0.0f;
+  auto fold = [&](int n, const float* ms, const float* ls, const float* os) {
+    float m_new = m_run;
+    for (int u = 0; u < n; ++u) m_new = fmaxf(m_new, ms[u]);
+    if (m_new == kNegInf) return;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    l_run *= alpha;
+    o_run *= alpha;
+    for (int u = 0; u < n; ++u) {
+      const float w = __builtin_amdgcn_exp2f(ms[u] - m_new);
+      l_run += w * ls[u];
+      o_run += w * os[u];
+    }
+    m_run = m_new;
+  };
   int s = grp;
   for (; s + 3 * GROUPS < S; s += 4 * GROUPS) {
+    float ms[4], ls[4], os[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int su = s + u * GROUPS;
-      acc[u] += w_s[su] * d.part_o[(p0 + (int64_t)su * d.rows) * D + dim];
+      const int64_t p = p0 + (int64_t)(s + u * GROUPS) * d.rows;
+      ms[u] = d.part_ml[2 * p];
+      ls[u] = d.part_ml[2 * p + 1];
+      os[u] = d.part_o[p * D + dim];
     }
+    fold(4, ms, ls, os);
   }
-  for (; s < S; s += GROUPS) acc[0] += w_s[s] * d.part_o[(p0 + (int64_t)s * d.rows) * D + dim];
-  o_part[grp][dim] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  for (; s < S; s += GROUPS) {
+    const int64_t p = p0 + (int64_t)s * d.rows;
+    const float ms = d.part_ml[2 * p], ls = d.part_ml[2 * p + 1], os = d.part_o[p * D + dim];
+    fold(1, &ms, &ls, &os);
+  }
+  if (dim == 0) {
+    m_grp[grp] = m_run;
+    l_grp[grp] = l_run;
+  }
+  o_grp[grp][dim] = o_run;
   __syncthreads();
   if (grp != 0) return;
-  float o = 0.0f;
+  float M = m_grp[0];
 #pragma unroll
-  for (int q = 0; q < GROUPS; ++q) o += o_part[q][dim];
+  for (int q = 1; q < GROUPS; ++q) M = fmaxf(M, m_grp[q]);
+  float o = 0.0f, Ltot = 0.0f;
+  if (M != kNegInf) {
+#pragma unroll
+    for (int q = 0; q < GROUPS; ++q) {
+      const float w = __builtin_amdgcn_exp2f(m_grp[q] - M);
+      o += w * o_grp[q][dim];
+      Ltot += w * l_grp[q];
+    }
+  }
   const float inv = (Ltot > 0.0f) ? (1.0f / Ltot) : 0.0f;
   a.o[b * a.osb + hq * a.osh + (int64_t)qi * a.osn + dim] = Elem<BF16>::round(o * inv);
   if (a.lse != nullptr && dim == 0) {
