@@ -76,6 +76,11 @@ CASES = [
     (1, 2, 1, 300, 77, 64, "bottom_right"),  # rows that see no key
     (1, 2, 2, 70, 300, 128, True),       # top-left with Nq < Nk: keys no query sees
     (1, 8, 8, 1024, 1024, 128, True),
+    # dQ kernel: key tiles no row of a query block masks (below its diagonal,
+    # inside the keys) run in a loop of their own; with these diagonals that
+    # loop ends after an even or an odd number of tiles, depending on the block
+    (1, 2, 1, 200, 600, 64, "bottom_right"),
+    (1, 4, 2, 150, 500, 128, "bottom_right"),
 ]
 
 
