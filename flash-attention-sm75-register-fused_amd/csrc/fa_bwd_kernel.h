@@ -580,10 +580,10 @@ __global__ void __launch_bounds__(512, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
 // The forward's work decomposition (block_work; causal: largest block
 // first): wave w owns query rows q0 + 32w .. +32 and walks the 64-key tiles
 // its block can see, K and V tiles double buffered through LDS.  Two
-// workgroups per CU (238 VGPRs, 80 KiB of LDS each): measured 26% faster
-// than one on the C4 training shape.
-// Two workgroups per CU, except with a mask at head_dim 128 (its mask words
-// do not fit the 256 registers that allows).
+// workgroups per CU (at most 256 VGPRs, 80 KiB of LDS each): measured 26%
+// faster than one on the C4 training shape; with a mask at head_dim 128 one
+// (its mask words do not fit those registers).  The tiles no row of the
+// block masks run in a loop of their own, free of mask code.
 template <int D, bool CAUSAL, bool MASK, bool BF16>
 __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kernel(const BwdArgs a) {
   using L = Lds<D>;
