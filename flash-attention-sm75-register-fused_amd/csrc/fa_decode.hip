@@ -492,6 +492,125 @@ __global__ void __launch_bounds__(kCombineThreads) fa_decode_combine(const DecAr
   }
 }
 
+// Launches whose threads would each walk more than a few batches of splits
+// in fa_decode_combine (split count times head_dim at least
+// kWideCombineMin; e.g. one KV head of 65536 keys at 256 splits, whose
+// combine took 23 us that way) take this variant: one workgroup per (unit,
+// query column, 32 dimensions), 256 threads = 32 split groups x 8 lanes, lane
+// i taking dimensions 4i..4i+3 of the chunk (a float4 of each split's
+// partial O) and group g the splits g, g + 32, ... with up to 8 loads in
+// flight per thread; the groups' states merge once through LDS.  For few
+// splits its many small workgroups cost more than they save (a 16-column
+// GQA decode with 4 splits: 14% slower), hence the threshold.
+constexpr int kWideLanes = 8;                              // float4 lanes: 32 dims
+constexpr int kWideGroups = kCombineThreads / kWideLanes;  // split groups
+constexpr int kWideBatch = 8;                              // splits in flight per thread
+constexpr int kWideCombineMin = 4096;                      // splits * head_dim
+
+template <int D, bool BF16>
+__global__ void __launch_bounds__(kCombineThreads) fa_decode_combine_wide(const DecArgs d) {
+  const FwdArgs& a = d.f;
+  constexpr int CHUNKS = D / (4 * kWideLanes);
+  __shared__ float m_grp[kWideGroups], l_grp[kWideGroups];
+  __shared__ float4 o_grp[kWideGroups][kWideLanes];
+  const int tid = threadIdx.x;
+  const int chunk = (int)blockIdx.x % CHUNKS;
+  const int uc = (int)blockIdx.x / CHUNKS;
+  const int unit = uc / d.rows;
+  const int c = uc - unit * d.rows;  // query column of the unit
+  const int hkv_count = a.hq / a.group;
+  const int bh = unit / d.row_blocks;
+  const int rb = unit - bh * d.row_blocks;
+  const int b = bh / hkv_count;
+  const int hkv = bh - b * hkv_count;
+  const int r = rb * kDecodeMaxRows + c;
+  if (r >= d.total_rows) return;  // whole workgroup: columns past the last row
+  const int g = r / a.n;
+  const int qi = r - g * a.n;
+  const int hq = hkv * a.group + g;
+  const int64_t p0 = (int64_t)unit * d.splits * d.rows + c;  // split s: p0 + s * rows
+  const int S = d.splits;
+
+  const int lane = tid % kWideLanes;
+  const int grp = tid / kWideLanes;
+  const int dim0 = 4 * (chunk * kWideLanes + lane);
+  constexpr float kNegInf = -__builtin_inff();
+  // Running state as in fa_decode_combine, for 4 dimensions.
+  float m_run = kNegInf, l_run = 0.0f;
+  float o_run[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s = grp; s < S; s += kWideBatch * kWideGroups) {
+    float ms[kWideBatch], ls[kWideBatch];
+    float4 os[kWideBatch];
+    int n = 0;  // splits of this batch (a prefix of the 8)
+#pragma unroll
+    for (int u = 0; u < kWideBatch; ++u) {
+      const int su = s + u * kWideGroups;
+      if (su < S) {
+        const int64_t p = p0 + (int64_t)su * d.rows;
+        const float2 ml = *(const float2*)(d.part_ml + 2 * p);
+        ms[u] = ml.x;
+        ls[u] = ml.y;
+        os[u] = *(const float4*)(d.part_o + p * D + dim0);
+        n = u + 1;
+      }
+    }
+    float m_new = m_run;
+#pragma unroll
+    for (int u = 0; u < kWideBatch; ++u)
+      if (u < n) m_new = fmaxf(m_new, ms[u]);
+    if (m_new == kNegInf) continue;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    l_run *= alpha;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o_run[e] *= alpha;
+#pragma unroll
+    for (int u = 0; u < kWideBatch; ++u) {
+      if (u < n) {
+        const float w = __builtin_amdgcn_exp2f(ms[u] - m_new);
+        l_run += w * ls[u];
+        o_run[0] += w * os[u].x;
+        o_run[1] += w * os[u].y;
+        o_run[2] += w * os[u].z;
+        o_run[3] += w * os[u].w;
+      }
+    }
+    m_run = m_new;
+  }
+  if (lane == 0) {
+    m_grp[grp] = m_run;
+    l_grp[grp] = l_run;
+  }
+  o_grp[grp][lane] = float4{o_run[0], o_run[1], o_run[2], o_run[3]};
+  __syncthreads();
+  if (grp != 0) return;
+  float M = m_grp[0];
+#pragma unroll
+  for (int q = 1; q < kWideGroups; ++q) M = fmaxf(M, m_grp[q]);
+  float o[4] = {0.0f, 0.0f, 0.0f, 0.0f}, Ltot = 0.0f;
+  if (M != kNegInf) {
+#pragma unroll 8
+    for (int q = 0; q < kWideGroups; ++q) {
+      const float w = __builtin_amdgcn_exp2f(m_grp[q] - M);
+      const float4 oq = o_grp[q][lane];
+      o[0] += w * oq.x;
+      o[1] += w * oq.y;
+      o[2] += w * oq.z;
+      o[3] += w * oq.w;
+      Ltot += w * l_grp[q];
+    }
+  }
+  const float inv = (Ltot > 0.0f) ? (1.0f / Ltot) : 0.0f;
+  half4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = Elem<BF16>::round(o[e] * inv);
+  *(half4*)(a.o + b * a.osb + hq * a.osh + (int64_t)qi * a.osn + dim0) = v;
+  if (a.lse != nullptr && chunk == 0 && lane == 0) {
+    const float m_use = (M == kNegInf) ? 0.0f : M;
+    a.lse[((int64_t)b * a.hq + hq) * a.n + qi] =
+        (m_use + __builtin_log2f(Ltot)) * 0.69314718055994530942f;
+  }
+}
+
 template <bool BF16>
 void launch_decode_typed(const DecArgs& d, const DecodePlan& pl, int head_dim, bool causal,
                          hipStream_t stream) {
@@ -508,14 +627,18 @@ void launch_decode_typed(const DecArgs& d, const DecodePlan& pl, int head_dim, b
 #undef FA_DEC_M
 #undef FA_DEC
   if (pl.splits > 1) {
-    const dim3 cgrid((unsigned)((int64_t)pl.units * pl.rows));
-    if (head_dim == 128)
-      hipLaunchKernelGGL((fa_decode_combine<128, BF16>), cgrid, dim3(kCombineThreads), 0, stream,
-                         d);
-    else
-      hipLaunchKernelGGL((fa_decode_combine<64, BF16>), cgrid, dim3(kCombineThreads), 0, stream,
-                         d);
+    const bool wide = pl.splits * head_dim >= kWideCombineMin;
+    const dim3 cgrid((unsigned)((int64_t)pl.units * pl.rows * (wide ? head_dim / 32 : 1)));
+#define FA_CMB(DD)                                                                          \
+  if (wide)                                                                                 \
+    hipLaunchKernelGGL((fa_decode_combine_wide<DD, BF16>), cgrid, dim3(kCombineThreads), 0, \
+                       stream, d);                                                          \
+  else                                                                                      \
+    hipLaunchKernelGGL((fa_decode_combine<DD, BF16>), cgrid, dim3(kCombineThreads), 0, stream, d)
+    if (head_dim == 128) { FA_CMB(128); } else { FA_CMB(64); }
+#undef FA_CMB
   }
+
 }
 
 }  // namespace

@@ -48,6 +48,7 @@ CASES = [
     (1, 64, 8, 4, 5000, 128, "bottom_right"),  # 4 draft tokens: 32 rows
     (3, 8, 8, 2, 77, 64, "top_left"),
     (1, 32, 1, 1, 60000, 128, False),     # long context, one KV head (MQA)
+    (1, 7, 1, 1, 50000, 64, "bottom_right"),  # 195 splits: the wide combine at d64
     (2, 4, 2, 1, 1, 128, False),          # a single key
     (2, 4, 2, 3, 31, 64, "bottom_right"),
     (2, 4, 2, 3, 33, 128, False),
