@@ -16,7 +16,8 @@
 //   * the four waves' (max, sum, O) merge through LDS at the end;
 //   * with one split the workgroup writes O (and LSE) directly; otherwise it
 //     writes an fp32 partial (unnormalised O, running max in log2 units, sum)
-//     to the caller's workspace and fa_decode_combine merges the splits.
+//     to the caller's workspace and fa_decode_combine (for many splits,
+//     fa_decode_combine_wide) merges the splits.
 //
 // Small launches (a 128-row prefill grid of at most kSmallLaunchItems
 // workgroups, e.g. one head of 512 rows) take the same path with the query
