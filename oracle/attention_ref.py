@@ -217,7 +217,8 @@ def attention_f64(Q, K, V, causal=False, scale=None, attn_mask=None):
     return np.matmul(E / np.where(tot > 0, tot, 1.0), v)
 
 
-def attention_backward_f64(Q, K, V, dO, causal=False, scale=None, attn_mask=None):
+def attention_backward_f64(Q, K, V, dO, causal=False, scale=None, attn_mask=None,
+                           delta_from_o=None):
     """Gradients (dQ, dK, dV) of attention_f64's O in float64, closed form.
 
     No reference counterpart: the reference's autograd backward raises
@@ -230,6 +231,13 @@ def attention_backward_f64(Q, K, V, dO, causal=False, scale=None, attn_mask=None
     that see no key have P = 0 and contribute nothing.  ``attn_mask``: a
     boolean mask (True = visible) broadcastable to [B, Hq, Nq, Nk], as in
     :func:`attention_reference`.
+
+    ``delta_from_o``: an output O [B, Hq, Nq, D] (e.g. the forward's rounded
+    one) from which the row term is taken as rowsum(dO o O) instead, the
+    form a fused backward evaluates (rowsum(dP o P) = rowsum(dO o O) for the
+    exact O).  Everything else stays exact, so this isolates what O's
+    rounding does to the gradients, which is large where dP - rowsum
+    nearly cancels (rows that see one or two keys of a peaked softmax).
     """
     Q = np.asarray(Q)
     K = np.asarray(K)
@@ -257,7 +265,11 @@ def attention_backward_f64(Q, K, V, dO, causal=False, scale=None, attn_mask=None
     P = E / np.where(tot > 0, tot, 1.0)
     dv = np.matmul(np.swapaxes(P, -1, -2), do)
     dP = np.matmul(do, np.swapaxes(v, -1, -2))
-    dS = P * (dP - (dP * P).sum(axis=-1, keepdims=True))
+    if delta_from_o is None:
+        delta = (dP * P).sum(axis=-1, keepdims=True)
+    else:
+        delta = (do * np.asarray(delta_from_o).astype(np.float64)).sum(axis=-1, keepdims=True)
+    dS = P * (dP - delta)
     dq = float(scale) * np.matmul(dS, k)
     dk = float(scale) * np.matmul(np.swapaxes(dS, -1, -2), q)
     g = Hq // Hkv

@@ -1,0 +1,105 @@
+"""Randomized parity sweep over the forward (O, LSE) and backward (dQ, dK, dV).
+
+Each case draws, from a fixed seed, a batch, KV heads and GQA group, query and
+key lengths (decode-sized and larger, equal or not), head_dim 64 or 128, the
+causal mode (none, top-left, bottom-right), binary16 or bfloat16, a softmax
+scale (the default, 0.3, -0.125 or 0.05) and an optional boolean mask (key
+padding [B,1,1,Nk] or a full [B,Hq,Nq,Nk] one), and checks the kernels
+against the numpy oracle on the same inputs, with the bars of the dedicated
+tests:
+  * O: |O - O_ref| <= 2e-3 + 1e-2 |O_ref| (binary16), 4e-3 + 1.6e-2 |O_ref|
+    (bfloat16), O_ref in fp32;
+  * LSE: the same infinite entries, finite ones within 1e-3 + 1e-4 |LSE_ref|
+    (binary16) or log(1 + 2^-8) (bfloat16: the row sums add probabilities
+    rounded to 8 significant bits), LSE_ref in float64;
+  * gradients (cases with Nq <= 400 and Nk <= 800): |G - R| <= a max|R| +
+    r |R| with (a, r) = (2e-3, 1e-2) or (1e-2, 4e-2), R the float64 closed
+    form with the row term rowsum(dO o O) taken from the kernel's own O
+    (attention_backward_f64's delta_from_o), since for rows that see one or
+    two keys of a peaked softmax that term's cancellation makes the exact
+    gradient depend on O's rounding beyond the bar.
+"""
+import numpy as np
+import pytest
+import torch
+
+from flash_attention_sm75 import flash_attention, flash_attention_forward_ex
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+CAUSAL = {0: False, 1: True, 2: "bottom_right"}
+N_CASES = 80
+
+
+def draw(case):
+    rng = np.random.default_rng(1000 + case)
+    B = int(rng.integers(1, 4))
+    Hkv = int(rng.choice([1, 2, 4]))
+    Hq = Hkv * int(rng.choice([1, 2, 3, 4, 7, 8]))
+    Nq = int(rng.choice([1, 2, 3, 4])) if rng.random() < 0.3 else int(rng.integers(1, 700))
+    Nk = Nq if rng.random() < 0.4 else int(rng.integers(1, 2500))
+    D = int(rng.choice([64, 128]))
+    code = int(rng.integers(0, 3))
+    bf16 = bool(rng.random() < 0.3)
+    scale = None if rng.random() < 0.7 else float(rng.choice([0.3, -0.125, 0.05]))
+    mk = float(rng.random())
+    return B, Hq, Hkv, Nq, Nk, D, code, bf16, scale, mk
+
+
+@pytest.mark.parametrize("case", range(N_CASES))
+def test_random_case(device, case):
+    B, Hq, Hkv, Nq, Nk, D, code, bf16, scale, mk = draw(case)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    g = torch.Generator("cpu").manual_seed(case)
+    q = torch.randn(B, Hq, Nq, D, generator=g).to(dt)
+    k = torch.randn(B, Hkv, Nk, D, generator=g).to(dt)
+    v = torch.randn(B, Hkv, Nk, D, generator=g).to(dt)
+    mask = None
+    if mk < 0.15:
+        mask = torch.rand(B, 1, 1, Nk, generator=g) < 0.85
+    elif mk < 0.25:
+        mask = torch.rand(B, Hq, Nq, Nk, generator=g) < 0.7
+    print(f"[sweep {case}] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} causal={code} "
+          f"{'bf16' if bf16 else 'fp16'} scale={scale} "
+          f"mask={None if mask is None else tuple(mask.shape)}", flush=True)
+    npf = lambda t: t.float().cpu().numpy()
+    m_np = None if mask is None else mask.numpy()
+    md = None if mask is None else mask.to(device)
+    o, lse = flash_attention_forward_ex(q.to(device), k.to(device), v.to(device),
+                                        causal=CAUSAL[code], scale=scale, return_lse=True,
+                                        attn_mask=md)
+    torch.cuda.synchronize()
+    want = ref.attention_reference(npf(q), npf(k), npf(v), causal=code, scale=scale,
+                                   return_f32=True, attn_mask=m_np)
+    atol, rtol = (4e-3, 1.6e-2) if bf16 else (2e-3, 1e-2)
+    got = npf(o)
+    assert np.isfinite(got).all()
+    err = np.abs(got - want)
+    assert np.all(err <= atol + rtol * np.abs(want)), float(err.max())
+    lse_ref = ref.attention_lse(npf(q), npf(k), causal=code, scale=scale, attn_mask=m_np)
+    gl = lse.cpu().numpy()
+    fin = np.isfinite(lse_ref)
+    assert np.array_equal(np.isfinite(gl), fin)
+    if bf16:
+        np.testing.assert_allclose(gl[fin], lse_ref[fin], atol=float(np.log1p(2.0 ** -8)) + 1e-5,
+                                   rtol=0)
+    else:
+        np.testing.assert_allclose(gl[fin], lse_ref[fin], atol=1e-3, rtol=1e-4)
+    if Nq > 400 or Nk > 800:
+        return
+    leaves = [t.to(device).requires_grad_() for t in (q, k, v)]
+    do = torch.randn(B, Hq, Nq, D, generator=g).to(dt)
+    out = flash_attention(*leaves, causal=CAUSAL[code], scale=scale, attn_mask=md)
+    out.backward(do.to(device))
+    torch.cuda.synchronize()
+    wants = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=code, scale=scale,
+                                       attn_mask=m_np, delta_from_o=npf(out.detach()))
+    ba, br = (1e-2, 4e-2) if bf16 else (2e-3, 1e-2)
+    for name, leaf, w in zip(("dQ", "dK", "dV"), leaves, wants):
+        gg = npf(leaf.grad).astype(np.float64)
+        sc = max(float(np.abs(w).max()) if w.size else 0.0, 1e-2)
+        worst = float((np.abs(gg - w) / (ba * sc + br * np.abs(w) + 1e-30)).max()) if w.size else 0.0
+        print(f"  {name}: worst/bar={worst:.3f}", flush=True)
+        assert np.isfinite(gg).all(), name
+        assert worst <= 1.0, (name, worst)

@@ -176,3 +176,37 @@ def test_masked_matches_torch_autograd(mshape, causal):
     want = torch_grads(q, k, v, do, causal, ref.default_scale(64), attn_mask=mask)
     for name, g, w in zip(("dQ", "dK", "dV"), got, want):
         np.testing.assert_allclose(g, w, rtol=1e-9, atol=1e-11, err_msg=name)
+
+
+@pytest.mark.parametrize("causal", [False, True, "bottom_right"])
+def test_delta_from_o(causal):
+    """delta_from_o: with the exact O the row term rowsum(dO o O) equals
+    rowsum(dP o P), so the gradients are unchanged; with O + E every query
+    row i moves by -rowsum(dO_i o E_i) P_i in dS, so dQ and dK shift by that
+    term's products with K and Q (P from torch in float64) and dV not at all."""
+    B, Hq, Hkv, Nq, Nk, D = 1, 4, 2, 7, 11, 64
+    q, k, v = rnd((B, Hq, Nq, D), 21), rnd((B, Hkv, Nk, D), 22), rnd((B, Hkv, Nk, D), 23)
+    do = rnd((B, Hq, Nq, D), 24)
+    c = CODE[causal]
+    scale = ref.default_scale(D)
+    base = ref.attention_backward_f64(q, k, v, do, causal=c)
+    o = ref.attention_f64(q, k, v, causal=c)
+    same = ref.attention_backward_f64(q, k, v, do, causal=c, delta_from_o=o)
+    for g, w in zip(same, base):
+        np.testing.assert_allclose(g, w, rtol=1e-10, atol=1e-12)
+    e = np.random.default_rng(25).standard_normal(o.shape) * 1e-2
+    moved = ref.attention_backward_f64(q, k, v, do, causal=c, delta_from_o=o + e)
+    g = Hq // Hkv
+    K = torch.tensor(k.astype(np.float64)).repeat_interleave(g, 1)
+    Q = torch.tensor(q.astype(np.float64))
+    S = Q @ K.transpose(-1, -2) * scale
+    m = ref.causal_mask(Nq, Nk, c)
+    if m is not None:
+        S = S.masked_fill(torch.tensor(m), float("-inf"))
+    P = torch.softmax(S, -1).nan_to_num(0.0)
+    shift = -(torch.tensor(do.astype(np.float64)) * torch.tensor(e)).sum(-1, keepdim=True) * P
+    want_dq = base[0] + scale * (shift @ K).numpy()
+    want_dk = base[1] + scale * (shift.transpose(-1, -2) @ Q).numpy().reshape(B, Hkv, g, Nk, D).sum(2)
+    np.testing.assert_allclose(moved[0], want_dq, rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(moved[1], want_dk, rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(moved[2], base[2], rtol=0, atol=0)
