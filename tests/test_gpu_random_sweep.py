@@ -12,6 +12,9 @@ tests:
   * LSE: the same infinite entries, finite ones within 1e-3 + 1e-4 |LSE_ref|
     (binary16) or log(1 + 2^-8) (bfloat16: the row sums add probabilities
     rounded to 8 significant bits), LSE_ref in float64;
+  * inputs: with probability 0.4 (a separate seeded draw), Q, K and V are
+    [B, N, H, D] buffers viewed as [B, H, N, D] (the layout transformers
+    hands to SDPA), which the kernels read in place;
   * gradients (cases with Nq <= 400 and Nk <= 800): |G - R| <= a max|R| +
     r |R| with (a, r) = (2e-3, 1e-2) or (1e-2, 4e-2), R the float64 closed
     form with the row term rowsum(dO o O) taken from the kernel's own O
@@ -55,6 +58,9 @@ def test_random_case(device, case):
     q = torch.randn(B, Hq, Nq, D, generator=g).to(dt)
     k = torch.randn(B, Hkv, Nk, D, generator=g).to(dt)
     v = torch.randn(B, Hkv, Nk, D, generator=g).to(dt)
+    strided = bool(np.random.default_rng(5000 + case).random() < 0.4)
+    if strided:  # same values, [B, N, H, D] storage
+        q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
     mask = None
     if mk < 0.15:
         mask = torch.rand(B, 1, 1, Nk, generator=g) < 0.85
@@ -62,11 +68,15 @@ def test_random_case(device, case):
         mask = torch.rand(B, Hq, Nq, Nk, generator=g) < 0.7
     print(f"[sweep {case}] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} causal={code} "
           f"{'bf16' if bf16 else 'fp16'} scale={scale} "
-          f"mask={None if mask is None else tuple(mask.shape)}", flush=True)
+          f"mask={None if mask is None else tuple(mask.shape)} strided={strided}", flush=True)
     npf = lambda t: t.float().cpu().numpy()
     m_np = None if mask is None else mask.numpy()
     md = None if mask is None else mask.to(device)
-    o, lse = flash_attention_forward_ex(q.to(device), k.to(device), v.to(device),
+    qd, kd, vd = (t.to(device) for t in (q, k, v))  # .to keeps the strides
+    if strided:  # a size-1 dimension's stride does not matter
+        assert Nq == 1 or qd.stride(2) == Hq * D
+        assert Nk == 1 or kd.stride(2) == Hkv * D
+    o, lse = flash_attention_forward_ex(qd, kd, vd,
                                         causal=CAUSAL[code], scale=scale, return_lse=True,
                                         attn_mask=md)
     torch.cuda.synchronize()
@@ -88,7 +98,7 @@ def test_random_case(device, case):
         np.testing.assert_allclose(gl[fin], lse_ref[fin], atol=1e-3, rtol=1e-4)
     if Nq > 400 or Nk > 800:
         return
-    leaves = [t.to(device).requires_grad_() for t in (q, k, v)]
+    leaves = [t.detach().requires_grad_() for t in (qd, kd, vd)]
     do = torch.randn(B, Hq, Nq, D, generator=g).to(dt)
     out = flash_attention(*leaves, causal=CAUSAL[code], scale=scale, attn_mask=md)
     out.backward(do.to(device))
