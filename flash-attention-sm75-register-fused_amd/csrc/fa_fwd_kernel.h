@@ -80,14 +80,24 @@ namespace {
 // KV_SAME_STRIDE: K and V rows have the same stride, so the direct-load
 // offsets are shared (saves registers).  MASK: an explicit mask (one 64-bit
 // word per query row and tile, loaded a step ahead) hides keys too.
-template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, bool MASK, bool KSPLIT, bool BF16>
+// ROWSUM: the row sums of P come from the matrix pipe, as one more 32-row
+// output tile of O^T whose A operand is a row of ones (4 more MFMAs and 16
+// fewer VALU instructions per tile).  Launched for head_dim-64 causal
+// launches that hold every block at once: there a CU's large block runs its
+// last tiles alone, one wave per SIMD, and its step latency is the launch's
+// tail (measured: C3 +3.4%, B=1 Hq=14 Hkv=2 N=4096 +4.8%; launches that keep
+// two waves per SIMD busy throughout lose 1-2%, the extra matrix work costing
+// clock).
+template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, bool MASK, bool KSPLIT, bool BF16,
+          bool ROWSUM>
 __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
   using L = Lds<D>;
   using E = Elem<BF16>;
   constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
   constexpr int MT = D / 32;       // 32-row output tiles of O^T
+  constexpr int MTX = MT + (ROWSUM ? 1 : 0);  // P V output tiles, the row-sum tile last
   constexpr int NS = 2 * KK;       // S^T MFMAs per tile
-  constexpr int NPV = 4 * MT;      // P V MFMAs per tile
+  constexpr int NPV = 4 * MTX;     // P V MFMAs per tile
   constexpr int PFK = 3;           // K operand reads run this many MFMAs ahead
   constexpr int PFV = 2;           // V operand reads run this many MFMAs ahead
   constexpr int ROW_WAVES = KSPLIT ? 4 : WAVES;  // waves owning distinct rows
@@ -329,9 +339,17 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       const int off = ((kk & 1) ? k_base_odd : k_base_even) + 32 * t * L::Pitch + 32 * (kk >> 1);
       return *(const half8*)(Ks + off);
     };
-    // V^T operand v (16-key step ks = v / MT, output tile mt = v % MT).
+    // A operand of the row-sum tile (ROWSUM): row 0 all ones (lanes 0 and 32
+    // hold its two 8-key halves), rows 1-31 zero.  Row 0 of that tile's
+    // accumulator, lane c's register 0, is query c's sum of P; lanes 32-63
+    // hold row 4 there, which stays zero, so halves_sum of register 0 gives
+    // the sum in both lanes of the query.
+    const half8 ones_a = ql == 0 ? (half8)E::round(1.0f) : (half8)(_Float16)0;
+    // V^T operand v (16-key step ks = v / MTX, output tile mt = v % MTX; the
+    // row-sum tile mt = MT takes the constant operand).
     auto read_v = [&](const _Float16* Vs, int v) -> half8 {
-      const int ks = v / MT, mt = v % MT;
+      const int ks = v / MTX, mt = v % MTX;
+      if (ROWSUM && mt == MT) return ones_a;
       const int imm = 16 * ks * L::Pitch + 32 * mt;
       const half4 lo = ds_read_tr16(Vs + v_base0 + imm);
       const half4 hi4 = ds_read_tr16(Vs + v_base1 + imm);
@@ -341,8 +359,9 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     float16v oacc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) oacc[mt] = (float16v)0.0f;
+    float16v lacc = (float16v)0.0f;  // row-sum tile (ROWSUM)
     float m_run = -__builtin_inff();
-    float l_run = 0.0f;
+    float l_run = 0.0f;              // the lane's part of its row sum (VALU row sums)
     const float c2 = a.c;  // |scale| * log2(e)
 
     // S^T of two tiles in flight, ping-pong by the parity of the step's
@@ -400,7 +419,8 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
         const float alpha =
             (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * c2);
-        l_run *= alpha;
+        if constexpr (ROWSUM) lacc[0] *= alpha;  // its other entries stay 0
+        else l_run *= alpha;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) oacc[mt] *= alpha;
         m_run = m_new;
@@ -457,7 +477,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       // cannot (the last tile has no S MFMAs to hide them behind) go first.
       constexpr int NB = ns + NPV;                    // MFMA slots
       constexpr int PV_FIRST = ns;                    // slot of the first P V MFMA
-      constexpr int PAIR_SLOTS = NB - MT;             // slots available to pairs
+      constexpr int PAIR_SLOTS = NB - MTX;            // slots available to pairs
       half8 kf[NS];
       // P operands as 32-bit lanes: each converted pair is written whole
       // (inserting its two halves one by one makes the compiler convert and
@@ -466,7 +486,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       half8 vf[NPV];
       constexpr auto pair_slot = [](int p) constexpr {
         const int spread = (p * PAIR_SLOTS) / 16;
-        const int last_ok = PV_FIRST + (p / 4) * MT - 1;
+        const int last_ok = PV_FIRST + (p / 4) * MTX - 1;
         return spread < last_ok ? spread : last_ok;
       };
       // Row max of S_{j+1} over the lane's half of the row: element e
@@ -492,12 +512,14 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[t][i + 1], c2, -mc));
         const half2v pr = E::pack(p0, p1);
         pf[2 * t + (i >> 3)][(i & 7) >> 1] = __builtin_bit_cast(unsigned, pr);
-        l_run = E::sum2(pr, l_run);
-        // Keeps the row-sum update in this slot: left alone, the compiler
-        // sinks all 16 of a step's (serially dependent) updates, with
-        // repacks of their operands, to after the last MFMA, where nothing
-        // hides their latency.
-        asm volatile("" : "+v"(l_run));
+        if constexpr (!ROWSUM) {
+          l_run = E::sum2(pr, l_run);
+          // Keeps the row-sum update in this slot: left alone, the compiler
+          // sinks all 16 of a step's (serially dependent) updates, with
+          // repacks of their operands, to after the last MFMA, where nothing
+          // hides their latency.
+          asm volatile("" : "+v"(l_run));
+        }
       };
       static_for<16>([&](auto p_c) {
         if constexpr (pair_slot(decltype(p_c)::value) < 0) softmax_pair(p_c);
@@ -530,8 +552,11 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
           s_nxt[t] = E::mfma(kf[i], qf[kk], kk == 0 ? (float16v)0.0f : s_nxt[t]);
         } else {
           constexpr int v = slot - PV_FIRST;
-          constexpr int ks = v / MT, mt = v % MT;
-          oacc[mt] = E::mfma(vf[v], __builtin_bit_cast(half8, pf[ks]), oacc[mt]);
+          constexpr int ks = v / MTX, mt = v % MTX;
+          if constexpr (mt == MT)
+            lacc = E::mfma(vf[v], __builtin_bit_cast(half8, pf[ks]), lacc);
+          else
+            oacc[mt] = E::mfma(vf[v], __builtin_bit_cast(half8, pf[ks]), oacc[mt]);
         }
         if constexpr (HAS_NEXT) {
           static_for<LPW>([&](auto q_c) {
@@ -613,6 +638,9 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     }
     // No direct load may land in LDS after the workgroup ends.
     __builtin_amdgcn_s_waitcnt(0x0F70);
+    // From here on l_run is the lane's part of its row sum either way (the
+    // row-sum tile holds all of it in lanes 0-31, zero in lanes 32-63).
+    if constexpr (ROWSUM) l_run = lacc[0];
 
     if constexpr (KSPLIT) {
       // Group 1 wave w+4 hands its O (unnormalised), running max and partial
@@ -715,13 +743,20 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
   }
   const dim3 grid((unsigned)wgs);
   const dim3 block(64 * WAVES);
-#define FA_LAUNCH(C, S) \
-  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK, KSPLIT, BF16>), grid, block, 0, stream, \
+#define FA_LAUNCH(C, S, R)                                                                       \
+  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK, KSPLIT, BF16, R>), grid, block, 0, stream, \
                      args)
   if (causal) {
-    if (same) FA_LAUNCH(true, true); else FA_LAUNCH(true, false);
+    // Paired single-round launches at head_dim 64 take the ROWSUM instance.
+    if constexpr (D == 64 && WAVES == 4 && !MASK && !KSPLIT) {
+      if (args.pair_half > 0) {
+        if (same) FA_LAUNCH(true, true, true); else FA_LAUNCH(true, false, true);
+        return;
+      }
+    }
+    if (same) FA_LAUNCH(true, true, false); else FA_LAUNCH(true, false, false);
   } else {
-    if (same) FA_LAUNCH(false, true); else FA_LAUNCH(false, false);
+    if (same) FA_LAUNCH(false, true, false); else FA_LAUNCH(false, false, false);
   }
 #undef FA_LAUNCH
 }
