@@ -7,8 +7,13 @@ scale (the default, 0.3, -0.125 or 0.05) and an optional boolean mask (key
 padding [B,1,1,Nk] or a full [B,Hq,Nq,Nk] one), and checks the kernels
 against the numpy oracle on the same inputs, with the bars of the dedicated
 tests:
-  * O: |O - O_ref| <= 2e-3 + 1e-2 |O_ref| (binary16), 4e-3 + 1.6e-2 |O_ref|
-    (bfloat16), O_ref in fp32;
+  * O: |O - O_ref| <= 2e-3 + 1e-2 |O_ref| (binary16, O_ref in fp32); for
+    bfloat16 the first-order rounding bound 2^-8 (sum_j P_j |V_j| + 2 |O_ref|)
+    (each probability and the row sum rounded to 8 significant bits, then the
+    output), O_ref and sum_j P_j |V_j| (the oracle's attention over |V|) in
+    float64: the fixed bar of test_gpu_bf16 does not hold where a peaked row's
+    largest weights cancel in V (a sweep found 1.5e-2 at |O| = 0.001, 0.77 of
+    this bound);
   * LSE: the same infinite entries, finite ones within 1e-3 + 1e-4 |LSE_ref|
     (binary16) or log(1 + 2^-8) (bfloat16: the row sums add probabilities
     rounded to 8 significant bits), LSE_ref in float64;
@@ -82,11 +87,17 @@ def test_random_case(device, case):
     torch.cuda.synchronize()
     want = ref.attention_reference(npf(q), npf(k), npf(v), causal=code, scale=scale,
                                    return_f32=True, attn_mask=m_np)
-    atol, rtol = (4e-3, 1.6e-2) if bf16 else (2e-3, 1e-2)
     got = npf(o)
     assert np.isfinite(got).all()
+    if bf16:
+        want = ref.attention_f64(npf(q), npf(k), npf(v), causal=code, scale=scale, attn_mask=m_np)
+        spv = ref.attention_f64(npf(q), npf(k), np.abs(npf(v)), causal=code, scale=scale,
+                                attn_mask=m_np)
+        bound = 2.0 ** -8 * (spv + 2 * np.abs(want)) * 1.01 + 2e-6
+    else:
+        bound = 2e-3 + 1e-2 * np.abs(want)
     err = np.abs(got - want)
-    assert np.all(err <= atol + rtol * np.abs(want)), float(err.max())
+    assert np.all(err <= bound), float((err / bound).max())
     lse_ref = ref.attention_lse(npf(q), npf(k), causal=code, scale=scale, attn_mask=m_np)
     gl = lse.cpu().numpy()
     fin = np.isfinite(lse_ref)
