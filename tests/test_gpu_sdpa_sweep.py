@@ -1,0 +1,143 @@
+"""Randomized sweep of F.scaled_dot_product_attention with the patch applied.
+
+Each case draws, from a fixed seed, the arguments transformers and other
+callers hand to SDPA: batch, K/V heads and group size, query and key lengths
+(decode-sized and larger, equal or not), head_dim 64 or 128, binary16 or
+bfloat16, is_causal, enable_gqa, a softmax scale (the default, 0.3 or 0.05)
+and an optional mask (boolean key padding [B,1,1,Nk], a boolean [Nq,Nk] one,
+or an additive float one).  The patch's own routing rule decides the path:
+  * calls the kernel takes (boolean masks included, with or without
+    is_causal) are checked against the numpy oracle with torch's SDPA
+    semantics (is_causal = top-left, the mask ANDed with it, grouped heads
+    shared); bars as in the other sweeps: |O - O_ref| <= 2e-3 + 1e-2 |O_ref|
+    (binary16) or 2^-8 (sum_j P_j |V_j| + 2 |O_ref|) (bfloat16, the
+    first-order rounding bound, O_ref in float64); for about a third of them,
+    with inputs that require gradients, dQ/dK/dV through the patched call
+    against the float64 closed form (row term from the kernel's own O), at
+    |G - R| <= a max|R| + r |R| with (a, r) = (2e-3, 1e-2) or (1e-2, 4e-2);
+  * calls handed to torch (grouped heads without enable_gqa, additive masks)
+    must be counted as fallbacks with the predicted reason and give exactly
+    what the unpatched call gives (the same tensor, or the same exception)
+    wherever torch's own call gives the same tensor twice.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from flash_attention_sm75 import sdpa_patch as sp
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 60
+
+
+@pytest.fixture
+def patched():
+    sp.apply_patch()
+    sp.reset_stats()
+    try:
+        yield
+    finally:
+        sp.remove_patch()
+
+
+def draw(case):
+    rng = np.random.default_rng(7000 + case)
+    B = int(rng.integers(1, 3))
+    Hkv = int(rng.choice([1, 2, 4]))
+    grp = int(rng.choice([1, 2, 4, 7]))
+    Nq = int(rng.choice([1, 2, 5])) if rng.random() < 0.3 else int(rng.integers(1, 400))
+    Nk = Nq if rng.random() < 0.4 else int(rng.integers(1, 900))
+    D = int(rng.choice([64, 128]))
+    bf16 = bool(rng.random() < 0.3)
+    is_causal = bool(rng.random() < 0.4)
+    mk = float(rng.random())
+    enable_gqa = bool(grp > 1 and rng.random() < 0.85)
+    scale = None if rng.random() < 0.7 else float(rng.choice([0.3, 0.05]))
+    grad = bool(rng.random() < 0.35)
+    return B, Hkv * grp, Hkv, Nq, Nk, D, bf16, is_causal, mk, enable_gqa, scale, grad
+
+
+@pytest.mark.parametrize("case", range(N_CASES))
+def test_patched_sdpa_case(device, patched, case):
+    B, Hq, Hkv, Nq, Nk, D, bf16, is_causal, mk, enable_gqa, scale, grad = draw(case)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    g = torch.Generator("cpu").manual_seed(case)
+    q = torch.randn(B, Hq, Nq, D, generator=g).to(dt)
+    k = torch.randn(B, Hkv, Nk, D, generator=g).to(dt)
+    v = torch.randn(B, Hkv, Nk, D, generator=g).to(dt)
+    mask = None
+    if mk < 0.15:
+        mask = torch.rand(B, 1, 1, Nk, generator=g) < 0.85
+    elif mk < 0.25:
+        mask = torch.rand(Nq, Nk, generator=g) < 0.6
+    elif mk < 0.3:
+        mask = torch.randn(B, 1, Nq, Nk, generator=g).to(dt)  # additive: torch's
+    kw = {"enable_gqa": True} if enable_gqa else {}
+    print(f"[sdpa sweep {case}] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} "
+          f"{'bf16' if bf16 else 'fp16'} is_causal={is_causal} "
+          f"mask={None if mask is None else (tuple(mask.shape), str(mask.dtype))} "
+          f"gqa={enable_gqa} scale={scale} grad={grad}", flush=True)
+    qd, kd, vd = (t.to(device) for t in (q, k, v))
+    md = None if mask is None else mask.to(device)
+    reason = sp._fallback_reason(qd, kd, vd, md, 0.0, is_causal, kw)
+    if reason is not None:
+        errs, outs = [], []
+        for fn in (F.scaled_dot_product_attention, sp._original_sdpa, sp._original_sdpa):
+            try:
+                outs.append(fn(qd, kd, vd, attn_mask=md, is_causal=is_causal, scale=scale, **kw))
+                errs.append(None)
+            except RuntimeError as e:
+                outs.append(None)
+                errs.append(type(e).__name__)
+        torch.cuda.synchronize()
+        assert errs[0] == errs[1] == errs[2], errs
+        if errs[0] is None and torch.equal(outs[1], outs[2]):
+            assert torch.equal(outs[0], outs[1]), reason
+        elif errs[0] is None:  # torch's own call does not repeat: routing only
+            print("  torch's own call differs between two runs", flush=True)
+        s = sp.patch_stats()
+        assert (s["flash"], s["fallback"], s["fallback_reasons"]) == (0, 1, {reason: 1}), s
+        print(f"  fallback {reason}: same as unpatched ({errs[0] or 'returned'})", flush=True)
+        return
+
+    leaves = [t.detach().requires_grad_(grad) for t in (qd, kd, vd)]
+    o = F.scaled_dot_product_attention(*leaves, attn_mask=md, is_causal=is_causal, scale=scale,
+                                       **kw)
+    do = torch.randn(B, Hq, Nq, D, generator=g).to(dt)
+    if grad:
+        o.backward(do.to(device))
+    torch.cuda.synchronize()
+    s = sp.patch_stats()
+    assert (s["flash"], s["fallback"]) == (1, 0), s
+    npf = lambda t: t.detach().float().cpu().numpy()
+    code = 1 if is_causal else 0
+    m_np = None if mask is None else mask.numpy()
+    got = npf(o)
+    assert np.isfinite(got).all()
+    if bf16:
+        want = ref.attention_f64(npf(q), npf(k), npf(v), causal=code, scale=scale, attn_mask=m_np)
+        spv = ref.attention_f64(npf(q), npf(k), np.abs(npf(v)), causal=code, scale=scale,
+                                attn_mask=m_np)
+        bound = 2.0 ** -8 * (spv + 2 * np.abs(want)) * 1.01 + 2e-6
+    else:
+        want = ref.attention_reference(npf(q), npf(k), npf(v), causal=code, scale=scale,
+                                       return_f32=True, attn_mask=m_np)
+        bound = 2e-3 + 1e-2 * np.abs(want)
+    err = np.abs(got - want)
+    print(f"  O: worst/bound={float((err / bound).max()) if err.size else 0.0:.3f}", flush=True)
+    assert np.all(err <= bound)
+    if not grad:
+        return
+    wants = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), causal=code, scale=scale,
+                                       attn_mask=m_np, delta_from_o=got)
+    ba, br = (1e-2, 4e-2) if bf16 else (2e-3, 1e-2)
+    for name, leaf, w in zip(("dQ", "dK", "dV"), leaves, wants):
+        gg = npf(leaf.grad).astype(np.float64)
+        sc = max(float(np.abs(w).max()) if w.size else 0.0, 1e-2)
+        worst = float((np.abs(gg - w) / (ba * sc + br * np.abs(w) + 1e-30)).max()) if w.size else 0.0
+        print(f"  {name}: worst/bar={worst:.3f}", flush=True)
+        assert np.isfinite(gg).all(), name
+        assert worst <= 1.0, (name, worst)

@@ -381,3 +381,23 @@ def test_bool_mask_special_cases():
                                 return_f32=True),
         ref.attention_reference(q, k, v, attn_mask=(r | np.eye(12, dtype=bool)) & tril,
                                 return_f32=True), atol=0)
+
+
+@pytest.mark.parametrize("n_q,n_k,mshape", [(9, 30, (2, 1, 1, 30)), (30, 30, (30, 30)),
+                                            (13, 7, (2, 4, 13, 7))])
+def test_bool_mask_with_is_causal_matches_torch_sdpa_cpu(n_q, n_k, mshape):
+    """torch's CPU SDPA given both attn_mask and is_causal=True lets key j
+    reach query i iff the mask allows it and j <= i (top-left): the oracle's
+    causal=1 with the same mask."""
+    import torch
+    q = rnd((2, 4, n_q, 64), 58)
+    k = rnd((2, 2, n_k, 64), 59)
+    v = rnd((2, 2, n_k, 64), 60)
+    mask = np.random.default_rng(61).random(mshape) < 0.7
+    mask[..., 0] = True  # key 0 is visible to every row under top-left causal
+    got = ref.attention_reference(q, k, v, causal=1, attn_mask=mask, return_f32=True)
+    ke, ve = ref.expand_kv_for_gqa(q, k, v)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q).float(), torch.from_numpy(ke).float(), torch.from_numpy(ve).float(),
+        attn_mask=torch.from_numpy(np.ascontiguousarray(mask)), is_causal=True).numpy()
+    np.testing.assert_allclose(got, want, atol=2e-6)
