@@ -2,7 +2,7 @@
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
                   [--no-cpu-baseline] [--no-gemm-ceiling] [--all] [--decode] [--hf]
-                  [--shape B,Hq,Hkv,N,D,causal] [--no-backward] [--no-configs]
+                  [--shape B,Hq,Hkv,N,D,causal] [--no-backward] [--no-configs] [--no-widened]
 
 A step is one fused forward over one batch of synthetic input (the hot path:
 flash_attention_sm75.flash_attention_forward -> flash_attn_sm75_cuda ->
@@ -36,7 +36,11 @@ those calls over its wall time.  Besides the driver's keys the line holds
   backward      the backward pass (dQ, dK, dV) on the same workload: its
                 average time and TFLOPS at 2.5x the forward's FLOP count;
   decode        the split-K decode path (D1-D3: one query row per head
-                against a KV cache): median call time and HBM rate.
+                against a KV cache): median call time and HBM rate;
+  widened       the calls beyond the reference's fp16 square launches on the
+                C4 shape: bfloat16 forward and backward, a key-padding boolean
+                mask, and a chunked prefill (Nq=2048 against Nk=8192,
+                bottom-right causal): average call time and TFLOPS.
 Diagnostics go to stderr.
 """
 import argparse
@@ -406,6 +410,73 @@ def time_backward(cfg, steps=10, warmup=3, dtype="fp16", warm_ms=200.0):
     return a.elapsed_time(b) / steps
 
 
+def time_calls(fn, steps=20, warm_ms=100.0):
+    """Average ms of fn() over `steps` back-to-back calls, one HIP event pair
+    on the launch stream around them, after at least warm_ms of calls."""
+    import torch
+
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(steps):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def time_widened(steps=20):
+    """The calls the hot path was widened to, beyond the reference's fp16
+    square launches: bfloat16 forward and backward on the C4 shape, C4 with a
+    key-padding boolean mask (the masked kernel), and a chunked prefill
+    (2048 new rows against 8192 cached keys, bottom-right causal)."""
+    import torch
+
+    from flash_attention_sm75 import flash_attention_forward_ex
+
+    B, Hq, Hkv, N, D, causal, _, _ = CONFIGS["C4"]
+    dev = torch.device("cuda", 0)
+    F = flops(B, Hq, N, D, causal)
+    out = {}
+
+    g = torch.Generator("cpu").manual_seed(21)
+    q, k, v = (torch.randn(B, h, N, D, generator=g).to(torch.bfloat16).to(dev)
+               for h in (Hq, Hkv, Hkv))
+    ms = time_calls(lambda: flash_attention_forward_ex(q, k, v, causal=True), steps)
+    out["bf16_fwd"] = {"workload": "C4 shape in bfloat16", "ms": round(ms, 5),
+                       "tflops": round(F / (ms * 1e-3) / 1e12, 1)}
+    del q, k, v
+    bms = time_backward("C4", steps=10, warmup=3, dtype="bf16")
+    out["bf16_bwd"] = {"workload": "C4 shape in bfloat16, backward", "ms": round(bms, 5),
+                       "tflops": round(2.5 * F / (bms * 1e-3) / 1e12, 1),
+                       "flop_convention": "2.5x the forward's"}
+
+    q, k, v = (torch.randn(B, h, N, D, generator=g).half().to(dev) for h in (Hq, Hkv, Hkv))
+    mask = torch.ones(B, 1, 1, N, dtype=torch.bool, device=dev)
+    mask[..., N - N // 10:] = False  # the last 10% of keys are padding
+    ms = time_calls(lambda: flash_attention_forward_ex(q, k, v, causal=True, attn_mask=mask),
+                    steps)
+    out["mask_fwd"] = {"workload": "C4 shape, causal and a [B,1,1,N] key-padding mask "
+                                   "(last 10% hidden); FLOPs counted as unmasked causal",
+                       "ms": round(ms, 5), "tflops": round(F / (ms * 1e-3) / 1e12, 1)}
+
+    nq = 2048
+    qc = q[:, :, N - nq:].contiguous()
+    ms = time_calls(lambda: flash_attention_forward_ex(qc, k, v, causal="bottom_right"), steps)
+    visible = nq * (N - nq) + nq * (nq + 1) // 2
+    fc = 4 * B * Hq * D * visible
+    out["chunked_prefill"] = {"workload": f"B={B} Hq={Hq} Hkv={Hkv} Nq={nq} Nk={N} d={D}, "
+                                          "bottom-right causal",
+                              "ms": round(ms, 5), "tflops": round(fc / (ms * 1e-3) / 1e12, 1)}
+    return out
+
+
 def time_hf(prompt_len=4096, decode_steps=32):
     """Random-init Qwen2-0.5B-shaped model (no weights can be downloaded):
     prefill and teacher-forced KV-cache decode, unpatched vs patched SDPA."""
@@ -487,6 +558,8 @@ def main():
                     help="skip timing the other BASELINE configurations (C1-C5)")
     ap.add_argument("--no-backward", action="store_true",
                     help="skip timing the backward pass on the same workload")
+    ap.add_argument("--no-widened", action="store_true",
+                    help="skip timing the widened calls (bf16, boolean mask, chunked prefill)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise copy of 256 MiB (known HBM bytes) "
                          "to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
@@ -634,6 +707,11 @@ def main():
             }
         log(f"[decode] {decode}")
 
+    widened = None
+    if not args.no_widened and args.data == "randn" and cfg in CONFIGS:
+        widened = time_widened(args.steps)
+        log(f"[widened] {widened}")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.cpu_budget)
@@ -675,6 +753,7 @@ def main():
         "cpu_baseline": cpu,
         "backward": backward,
         "decode": decode,
+        "widened": widened,
     }
     print(json.dumps(line), flush=True)
 
