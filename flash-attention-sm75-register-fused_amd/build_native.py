@@ -39,6 +39,8 @@ HIP_SOURCES = [
     "fa_fwd_d64.hip", "fa_fwd_d64_mask.hip", "fa_fwd_d64_w8.hip", "fa_fwd_d64_ks.hip",
     "fa_fwd_d128_bf16.hip", "fa_fwd_d128_mask_bf16.hip", "fa_fwd_d128_ks_bf16.hip",
     "fa_fwd_d64_bf16.hip", "fa_fwd_d64_mask_bf16.hip", "fa_fwd_d64_ks_bf16.hip",
+    "fa_fwd_d128_keys.hip", "fa_fwd_d64_keys.hip", "fa_fwd_d128_keys_bf16.hip",
+    "fa_fwd_d64_keys_bf16.hip",
     "fa_bwd_d128.hip", "fa_bwd_d64.hip", "fa_bwd_d128_mask.hip", "fa_bwd_d64_mask.hip",
     "fa_bwd.hip",
     "fa_fwd.hip", "fa_decode.hip", "fa_mask.hip", "fa_naive.hip", "fa_capi.hip",

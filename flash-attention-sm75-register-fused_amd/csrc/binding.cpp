@@ -190,6 +190,24 @@ torch::Tensor pack_mask(const torch::Tensor& mask, const torch::Tensor& Q, int64
   return bits;
 }
 
+// The forward's mask: a key-padding mask (the same for every head and query
+// row, transformers' [B, 1, 1, Nk] for padded batches) goes to the kernels as
+// its bytes, read in place (no packing launch); any other shape is packed
+// into bit rows.  Returns the tensor the call's mask pointer refers to.
+torch::Tensor forward_mask(const torch::Tensor& mask, const torch::Tensor& Q, int64_t nk,
+                           fa_fwd_params& p) {
+  TORCH_CHECK(mask.dtype() == torch::kBool, "attn_mask must be a bool tensor");
+  TORCH_CHECK(mask.device() == Q.device(), "attn_mask must be on Q's device");
+  TORCH_CHECK(mask.dim() <= 4, "attn_mask must have at most 4 dimensions");
+  const auto m = mask.expand({Q.size(0), Q.size(1), Q.size(2), nk});
+  const bool per_key = (m.size(1) == 1 || m.stride(1) == 0) && (m.size(2) == 1 || m.stride(2) == 0);
+  if (!per_key) return pack_mask(mask, Q, nk, p);
+  p.mask_keys = reinterpret_cast<const uint8_t*>(m.data_ptr<bool>());
+  p.mask_keys_stride_b = m.size(0) > 1 ? m.stride(0) : 0;
+  p.mask_keys_stride_k = m.stride(3);
+  return mask;
+}
+
 std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_ex(
     torch::Tensor Q, torch::Tensor K, torch::Tensor V, int64_t causal, double scale,
     bool return_lse, c10::optional<torch::Tensor> attn_mask) {
@@ -240,7 +258,7 @@ std::tuple<torch::Tensor, c10::optional<torch::Tensor>> flash_attention_forward_
   p.scale = (float)scale;
   p.causal = (int)causal;
   torch::Tensor bits;  // lives until the launch is enqueued (stream-ordered reuse)
-  if (attn_mask.has_value()) bits = pack_mask(*attn_mask, Q, K.size(2), p);
+  if (attn_mask.has_value()) bits = forward_mask(*attn_mask, Q, K.size(2), p);
   forward_with_workspace(p, Q, "flash_attention_forward_ex");
   return {O, L};
 }

@@ -99,6 +99,14 @@ int validate(const fa_fwd_params* p, bool fused) {
                   "mask row stride %lld is below ceil(seq_len_kv / 64) = %lld words",
                   (long long)p->mask_stride_q, (long long)((kv_rows(p) + 63) / 64));
   }
+  if (p->mask_keys != nullptr) {
+    if (!fused)
+      return fail(FA_ERR_INVALID_ARGUMENT, "the naive path takes no mask");
+    if (p->mask_bits != nullptr)
+      return fail(FA_ERR_INVALID_ARGUMENT, "mask_bits and mask_keys are exclusive");
+    if (p->mask_keys_stride_b < 0 || p->mask_keys_stride_k < 0)
+      return fail(FA_ERR_INVALID_ARGUMENT, "mask_keys strides must be non-negative");
+  }
   const int64_t strides[12] = {p->q_stride_b, p->q_stride_h, p->q_stride_n,
                                p->k_stride_b, p->k_stride_h, p->k_stride_n,
                                p->v_stride_b, p->v_stride_h, p->v_stride_n,
@@ -162,6 +170,9 @@ fa::FwdArgs make_args(const fa_fwd_params* p) {
   a.msb = p->mask_stride_b;
   a.msh = p->mask_stride_h;
   a.msq = p->mask_stride_q;
+  a.mkeys = p->mask_keys;
+  a.mksb = p->mask_keys_stride_b;
+  a.mksk = p->mask_keys_stride_k;
   a.ctr = nullptr;
   a.items = 0;
   a.bf16 = p->dtype == FA_DTYPE_BF16 ? 1 : 0;

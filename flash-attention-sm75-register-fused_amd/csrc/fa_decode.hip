@@ -76,8 +76,14 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
-template <int D, bool CAUSAL, bool MASK, bool BF16>
+// MASK_MODE: 0 no explicit mask, 1 mask bits (one 32-bit word per row and
+// tile), 2 key-padding bytes (fa_fwd_params.mask_keys: one byte per key, the
+// same for every row of the batch; a ballot over the tile's 32 bytes forms
+// the word).
+template <int D, bool CAUSAL, int MASK_MODE, bool BF16>
 __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d) {
+  constexpr bool MASK = MASK_MODE != 0;
+  constexpr bool KEY_BYTES = MASK_MODE == 2;
   const FwdArgs& a = d.f;
   using L = DecLds<D>;
   using E = Elem<BF16>;
@@ -200,10 +206,16 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   // MASK: this lane's mask row read as 32-bit words (word t: keys of 32-key
   // tile t), through a buffer window over batch b's rows so the load is the
   // same kind as the K and V loads (their completion order is then the
-  // issue order, which the vmcnt wait below relies on).
+  // issue order, which the vmcnt wait below relies on).  KEY_BYTES: byte
+  // (tile * 32 + ql) of batch b's key row instead, one load per step too,
+  // through a window that ends at the last key (keys past it read as 0).
   __amdgpu_buffer_rsrc_t rmask;
   int m_voff = 0;
-  if (MASK) {
+  if (KEY_BYTES) {
+    const int64_t span = NK > 0 ? (int64_t)(NK - 1) * a.mksk + 1 : 0;
+    rmask = make_rsrc(a.mkeys + b * a.mksb, (int)min(span, (int64_t)INT32_MAX));
+    m_voff = ql * (int)a.mksk;
+  } else if (MASK) {
     const int hq_c = row_ok ? hq : hkv * a.group;
     const int qi_c = row_ok ? qi : 0;
     const int64_t words = (NK + 63) / 64;
@@ -214,6 +226,9 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   }
   auto load_mask = [&](int it, bool valid) -> uint32_t {
     const int tile = valid ? t_begin + wave + kWaves * it : t_begin;
+    if constexpr (KEY_BYTES)
+      return __builtin_amdgcn_raw_buffer_load_b8(rmask, m_voff + tile * kDecTile * (int)a.mksk,
+                                                 0, 0);
     return __builtin_amdgcn_raw_buffer_load_b32(rmask, m_voff + 4 * tile, 0, 0);
   };
 
@@ -254,6 +269,10 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     const int kstart = key0 + (wave + kWaves * it) * kDecTile;
     bool need_mask =
         (kstart + kDecTile > NK) || (CAUSAL && kstart + kDecTile - 1 > qi_lo + a.diag);
+    // Key bytes: lanes l and l + 32 hold key kstart + l, so the low half of
+    // the ballot is the tile's word (read here, after the next tile's loads
+    // are issued, as the word itself is).
+    if constexpr (KEY_BYTES) mw = (uint32_t)__builtin_amdgcn_ballot_w64(mw != 0);
     if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
     if (need_mask) {
       const uint32_t mws = mw >> (4 * hi);  // bit 8 (i / 4) + i % 4: element i
@@ -618,8 +637,10 @@ void launch_decode_typed(const DecArgs& d, const DecodePlan& pl, int head_dim, b
   const dim3 grid((unsigned)((int64_t)pl.units * pl.splits));
 #define FA_DEC(DD, C, M) \
   hipLaunchKernelGGL((fa_decode_kernel<DD, C, M, BF16>), grid, dim3(kThreads), 0, stream, d)
-#define FA_DEC_M(DD, C) \
-  if (d.f.mbits != nullptr) FA_DEC(DD, C, true); else FA_DEC(DD, C, false)
+#define FA_DEC_M(DD, C)                            \
+  if (d.f.mkeys != nullptr) FA_DEC(DD, C, 2);      \
+  else if (d.f.mbits != nullptr) FA_DEC(DD, C, 1); \
+  else FA_DEC(DD, C, 0)
   if (head_dim == 128) {
     if (causal) { FA_DEC_M(128, true); } else { FA_DEC_M(128, false); }
   } else {
@@ -658,6 +679,8 @@ bool decode_eligible(const FwdArgs& a, int batch) {
         ((int64_t)(a.hq - 1) * a.msh + (int64_t)(a.n - 1) * a.msq + words) * 8;
     if (span > (int64_t)INT32_MAX) return false;
   }
+  // Key bytes: 32-bit offsets up to one tile past the last key.
+  if (a.mkeys != nullptr && ((int64_t)a.nk + 64) * a.mksk > (int64_t)INT32_MAX) return false;
   return true;
 }
 

@@ -18,7 +18,7 @@ __global__ void fa_clear_tickets(uint64_t* ctr) {
   for (int i = threadIdx.x; i < kNumXcds; i += blockDim.x) ctr[i * kCtrStride] = 0ull;
 }
 
-template <int WAVES, bool MASK, bool KSPLIT, bool BF16>
+template <int WAVES, int MASK, bool KSPLIT, bool BF16>
 void launch_shape(const FwdArgs& a, int batch, int head_dim, bool causal, Schedule schedule,
                   hipStream_t stream) {
   if (head_dim == 128)
@@ -37,20 +37,24 @@ template <bool BF16>
 void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int policy,
                   hipStream_t stream) {
   const Schedule schedule = schedule_of_policy(policy);
+  if (a.mkeys != nullptr) {
+    launch_shape<4, 2, false, BF16>(a, batch, head_dim, causal, schedule, stream);
+    return;
+  }
   if (a.mbits != nullptr) {
-    launch_shape<4, true, false, BF16>(a, batch, head_dim, causal, schedule, stream);
+    launch_shape<4, 1, false, BF16>(a, batch, head_dim, causal, schedule, stream);
     return;
   }
   if constexpr (!BF16) {
     if (policy == 2) {
-      launch_shape<8, false, false, false>(a, batch, head_dim, causal, Schedule::kStatic, stream);
+      launch_shape<8, 0, false, false>(a, batch, head_dim, causal, Schedule::kStatic, stream);
       return;
     }
   }
   if (use_key_split(a, batch, head_dim, causal, policy))
-    launch_shape<8, false, true, BF16>(a, batch, head_dim, causal, Schedule::kStatic, stream);
+    launch_shape<8, 0, true, BF16>(a, batch, head_dim, causal, Schedule::kStatic, stream);
   else
-    launch_shape<4, false, false, BF16>(a, batch, head_dim, causal, schedule, stream);
+    launch_shape<4, 0, false, BF16>(a, batch, head_dim, causal, schedule, stream);
 }
 
 }  // namespace
@@ -120,7 +124,7 @@ constexpr int kSplitMinBlocks = 32;
 }  // namespace
 
 bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy) {
-  if (a.mbits != nullptr) return false;
+  if (has_mask(a)) return false;
   if (policy == 4) return true;
   if (policy != 0 || !causal || head_dim != 128) return false;
   FwdArgs planned = a;

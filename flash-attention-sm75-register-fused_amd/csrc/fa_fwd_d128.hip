@@ -2,6 +2,6 @@
 #include "fa_fwd_kernel.h"
 
 namespace fa {
-template void launch_fused<128, 4, false, false, false>(const FwdArgs&, int, bool, Schedule,
+template void launch_fused<128, 4, 0, false, false>(const FwdArgs&, int, bool, Schedule,
                                                       hipStream_t);
 }  // namespace fa

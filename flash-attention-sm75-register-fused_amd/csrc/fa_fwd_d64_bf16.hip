@@ -2,6 +2,6 @@
 #include "fa_fwd_kernel.h"
 
 namespace fa {
-template void launch_fused<64, 4, false, false, true>(const FwdArgs&, int, bool, Schedule,
+template void launch_fused<64, 4, 0, false, true>(const FwdArgs&, int, bool, Schedule,
                                                       hipStream_t);
 }  // namespace fa

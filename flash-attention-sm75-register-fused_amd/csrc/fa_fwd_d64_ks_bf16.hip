@@ -2,6 +2,6 @@
 #include "fa_fwd_kernel.h"
 
 namespace fa {
-template void launch_fused<64, 8, false, true, true>(const FwdArgs&, int, bool, Schedule,
+template void launch_fused<64, 8, 0, true, true>(const FwdArgs&, int, bool, Schedule,
                                                       hipStream_t);
 }  // namespace fa

@@ -78,8 +78,10 @@ namespace {
 //     through LDS, which merges and stores.  This halves the longest chain
 //     of steps in launches whose time is set by their largest causal block.
 // KV_SAME_STRIDE: K and V rows have the same stride, so the direct-load
-// offsets are shared (saves registers).  MASK: an explicit mask (one 64-bit
-// word per query row and tile, loaded a step ahead) hides keys too.
+// offsets are shared (saves registers).  MASK_MODE 1: an explicit mask (one
+// 64-bit word per query row and tile, loaded a step ahead) hides keys too;
+// MASK_MODE 2: a key-padding mask read as bytes (one per lane and tile, loaded
+// a step ahead; a ballot over the wave forms the same word).
 // ROWSUM: the row sums of P come from the matrix pipe, as one more 32-row
 // output tile of O^T whose A operand is a row of ones (4 more MFMAs and 16
 // fewer VALU instructions per tile).  Launched for head_dim-64 causal
@@ -88,9 +90,11 @@ namespace {
 // tail (measured: C3 +3.4%, B=1 Hq=14 Hkv=2 N=4096 +4.8%; launches that keep
 // two waves per SIMD busy throughout lose 1-2%, the extra matrix work costing
 // clock).
-template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, bool MASK, bool KSPLIT, bool BF16,
+template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, int MASK_MODE, bool KSPLIT, bool BF16,
           bool ROWSUM>
 __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
+  constexpr bool MASK = MASK_MODE != 0;        // an explicit mask: bits or key bytes
+  constexpr bool KEY_BYTES = MASK_MODE == 2;   // key-padding bytes (a.mkeys)
   using L = Lds<D>;
   using E = Elem<BF16>;
   constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
@@ -226,9 +230,22 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     const int NK = a.nk;  // key rows
 
     const _Float16* Qp = a.q + b * a.qsb + hq * a.qsh;
-    // Mask bits of this lane's query row (rows past N read row N - 1).
+    // Mask bits of this lane's query row (rows past N read row N - 1), or
+    // (key-padding bytes, a.mkeys) batch b's key row: lane l reads key
+    // 64 j + l of tile j and a ballot forms the tile's word.
     const uint64_t* mrow =
-        MASK ? a.mbits + b * a.msb + hq * a.msh + (int64_t)min(qrow, N - 1) * a.msq : nullptr;
+        MASK && !KEY_BYTES
+            ? a.mbits + b * a.msb + hq * a.msh + (int64_t)min(qrow, N - 1) * a.msq
+            : nullptr;
+    const uint8_t* krow = KEY_BYTES ? a.mkeys + b * a.mksb : nullptr;
+    // What a step loads ahead for tile j: the lane's mask word, or its key
+    // byte (lanes past the last key read the last key's byte, an
+    // unconditional load; those keys are hidden by the sequence-end mask
+    // whatever their bit says).
+    auto mask_ahead = [&](int j) -> uint64_t {
+      if constexpr (KEY_BYTES) return krow[(int64_t)min(j * kBlockN + lane, NK - 1) * a.mksk];
+      else return mrow[j];
+    };
     const _Float16* Kp = a.k + b * a.ksb + hkv * a.ksh;
     const _Float16* Vp = a.v + b * a.vsb + hkv * a.vsh;
 
@@ -390,8 +407,10 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // lane's max over its half of the row (the two wave halves hold the
     // row's other 16 keys of each 32-key sub-tile; the threshold test needs
     // no exchange between them, the rare rescale does).  mw: the lane's mask
-    // word of tile j (bit k: key 64 j + k visible).
+    // word of tile j (bit k: key 64 j + k visible), or its key byte (key-padding
+    // bytes), from which the wave's ballot forms that word.
     auto prepare = [&](int j, float16v (&s)[2], float mx, uint64_t mw) {
+      if constexpr (KEY_BYTES) mw = __builtin_amdgcn_ballot_w64(mw != 0);
       const int kstart = j * kBlockN;
       bool need_mask =
           (kstart + kBlockN > NK) || (CAUSAL && kstart + kBlockN - 1 > qw + a.diag);
@@ -455,7 +474,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       if (HAS_NEXT) {
         rk_next = k_window(j + STAGES);
         rv_next = v_window(j + STAGES - 1);
-        if (MASK) mw_next = mrow[j + 1];  // consumed by prepare(j + 1) at the end
+        if (MASK) mw_next = mask_ahead(j + 1);  // consumed by prepare(j + 1) at the end
       }
       _Float16* k_dst = kbuf(std::integral_constant<int, U>{});
       _Float16* v_dst = vbuf(std::integral_constant<int, U + STAGES - 1>{});
@@ -607,7 +626,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         for (int kk = 0; kk < KK; ++kk)
           s_buf[0][t] = E::mfma(read_k(k_first, t * KK + kk), qf[kk], s_buf[0][t]);
       }
-      prepare(tile0, s_buf[0], row_max(s_buf[0]), MASK ? mrow[tile0] : ~0ull);
+      prepare(tile0, s_buf[0], row_max(s_buf[0]), MASK ? mask_ahead(tile0) : ~0ull);
       // Step 0 loads K_STAGES into K_0's buffer: every wave must be done
       // reading it for S_0 first.
       __syncthreads();
@@ -724,7 +743,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
 // The dynamic schedule (use_dynamic_schedule) needs ticket counters in
 // a.ctr; they are cleared first, and the grid is one workgroup per resident
 // slot.
-template <int D, int WAVES, bool MASK, bool KSPLIT, bool BF16>
+template <int D, int WAVES, int MASK, bool KSPLIT, bool BF16>
 void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream) {
   const bool same = a.ksn == a.vsn;

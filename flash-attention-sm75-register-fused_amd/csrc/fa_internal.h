@@ -33,11 +33,17 @@ struct FwdArgs {
   int negate_q;     // scale < 0: Q fragments are negated (exact in fp16)
   const uint64_t* mbits;   // explicit mask bits or nullptr (see fa_fwd_params)
   int64_t msb, msh, msq;   // its strides in 64-bit words
+  const uint8_t* mkeys;    // key-padding mask bytes or nullptr (fa_fwd_params.mask_keys);
+  int64_t mksb, mksk;      //   exclusive with mbits; its batch and key strides in bytes
   uint64_t* ctr;    // queue counters of the dynamic schedule, or nullptr (static)
   int items;        // work items (query blocks): filled by the launcher
   int bf16;         // elements are bfloat16 (else binary16)
   int pair_half;    // > 0: single-round causal order pairing (launcher; block_work)
 };
+
+// Whether a call carries an explicit mask (bits or key-padding bytes): the
+// kernels' MASK instances serve both.
+inline bool has_mask(const FwdArgs& a) { return a.mbits != nullptr || a.mkeys != nullptr; }
 
 // Dynamic schedule of the fused kernel: one 64-bit (head, tail) counter per
 // XCD queue, kCtrStride counters (256 bytes) apart, in a caller workspace of
@@ -83,9 +89,10 @@ bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedu
 int64_t fused_workspace_bytes(const FwdArgs& a, int batch, int head_dim, bool causal,
                               int policy);
 // One instance family of the fused kernel (fa_fwd_kernel.h), explicitly
-// instantiated in fa_fwd_d*.hip.  KSPLIT: 8 waves on 128 rows, the two
-// groups of 4 splitting the key tiles.
-template <int D, int WAVES, bool MASK, bool KSPLIT, bool BF16>
+// instantiated in fa_fwd_d*.hip.  MASK: 0 none, 1 mask bits (a.mbits), 2
+// key-padding bytes (a.mkeys).  KSPLIT: 8 waves on 128 rows, the two groups
+// of 4 splitting the key tiles.
+template <int D, int WAVES, int MASK, bool KSPLIT, bool BF16>
 void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream);
 // Whether a call runs on key-split workgroups: policy 4, or AUTO for causal

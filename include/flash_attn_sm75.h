@@ -107,6 +107,17 @@ typedef struct fa_fwd_params {
   int64_t mask_stride_b, mask_stride_h, mask_stride_q;
   int dtype;          /* an fa_dtype (0, binary16, in a zeroed struct); the
                          naive path and the reference launchers are binary16 */
+  /* Optional key-padding mask read in place, or NULL: byte (b, j) at
+   * mask_keys + b * mask_keys_stride_b + j * mask_keys_stride_k, nonzero
+   * <=> key j is visible to every query row of every head of batch b (torch
+   * SDPA's boolean attn_mask of shape [B, 1, 1, Nk], [1, Nk] or [Nk], as
+   * transformers builds it for padded batches).  The kernels read one byte
+   * per key and form the words of mask_bits themselves, so a call needs no
+   * fa_sm75_pack_mask launch.  Strides in bytes, non-negative (0 broadcasts
+   * the batch).  Exclusive with mask_bits; combines (AND) with `causal`.
+   * No reference counterpart (the reference takes no mask). */
+  const uint8_t* mask_keys;
+  int64_t mask_keys_stride_b, mask_keys_stride_k;
 } fa_fwd_params;
 
 /* Fills strides for contiguous [B,H,N,D] Q/O and [B,Hkv,Nk,D] K/V tensors. */
@@ -259,7 +270,7 @@ int fa_sm75_backward(const fa_bwd_params* p);
  * or p is NULL). */
 int64_t fa_sm75_backward_workspace_size(const fa_bwd_params* p);
 
-#define FA_SM75_ABI_VERSION 4
+#define FA_SM75_ABI_VERSION 5
 
 /* ---- Reference launcher signatures ------------------------------------ */
 

@@ -23,6 +23,8 @@ class Params(ctypes.Structure):
         ("mask_bits", ctypes.c_void_p), ("mask_stride_b", ctypes.c_int64),
         ("mask_stride_h", ctypes.c_int64), ("mask_stride_q", ctypes.c_int64),
         ("dtype", ctypes.c_int),
+        ("mask_keys", ctypes.c_void_p), ("mask_keys_stride_b", ctypes.c_int64),
+        ("mask_keys_stride_k", ctypes.c_int64),
     ]]
 
 

@@ -226,8 +226,23 @@ def test_mask_param_validation(lib):
     assert b"naive path takes no mask" in lib.fa_sm75_last_error()
 
 
+def test_mask_keys_validation(lib):
+    """Key-padding bytes: exclusive with mask_bits, non-negative strides, not
+    on the naive path (all rejected before any device work)."""
+    p = make(lib, mask_keys=0x1000, mask_bits=0x1000)
+    assert lib.fa_sm75_forward(ctypes.byref(p)) == 1
+    assert b"exclusive" in lib.fa_sm75_last_error()
+    for field in ("mask_keys_stride_b", "mask_keys_stride_k"):
+        p = make(lib, mask_keys=0x1001, **{field: -1})
+        assert lib.fa_sm75_forward(ctypes.byref(p)) == 1
+        assert b"mask_keys strides" in lib.fa_sm75_last_error()
+    p = make(lib, mask_keys=0x1001)
+    assert lib.fa_sm75_naive_forward(ctypes.byref(p), ctypes.c_void_p(0x1000)) == 1
+    assert b"naive path takes no mask" in lib.fa_sm75_last_error()
+
+
 def test_abi_version(lib):
-    assert lib.fa_sm75_abi_version() == 4
+    assert lib.fa_sm75_abi_version() == 5
 
 
 def test_kernel_policy_switch(lib):

@@ -76,6 +76,8 @@ CASES = [
     (2, 8, 2, 1, 5000, 128, (2, 1, 1, 5000), 0.7, False),  # decode + padding
     (2, 8, 2, 4, 3000, 64, (2, 8, 4, 3000), 0.5, "bottom_right"),  # split-K, per-head mask
     (1, 4, 4, 100, 100, 128, (100, 100), 0.02, False),  # sparse: empty rows
+    (2, 8, 2, 1, 3000, 64, (3000,), 0.6, False),  # 1-D key mask (key bytes, decode)
+    (2, 4, 4, 130, 700, 128, (1, 700), 0.7, True),  # [1, Nk] (key bytes, prefill)
 ]
 
 
@@ -184,3 +186,107 @@ def test_tiny_qwen2_left_padded_batch(device):
     scale = plain.abs().max().item()
     print(f"  max |dlogit| = {diff:.3e} (max |logit| {scale:.3e})", flush=True)
     assert diff <= 1e-3 + 2e-2 * scale
+
+
+def test_strided_key_padding_view(device):
+    """A [B, 1, 1, Nk] key-padding view with key stride 2 (every other
+    column of a wider buffer) is read in place as key bytes."""
+    B, Hq, Hkv, Nq, Nk, D = 2, 8, 2, 1, 2500, 128
+    q, k, v = seeded((B, Hq, Nq, D), 41), seeded((B, Hkv, Nk, D), 42), seeded((B, Hkv, Nk, D), 43)
+    wide = rand_mask((B, 1, 1, 2 * Nk), 0.7, 44)
+    m = wide[..., ::2]
+    for nq in (1, 200):  # split-K and prefill kernels
+        qq = seeded((B, Hq, nq, D), 45)
+        o = flash_attention_forward_ex(qq.to(device), k.to(device), v.to(device),
+                                       attn_mask=wide.to(device)[..., ::2])
+        torch.cuda.synchronize()
+        expect = ref.attention_reference(qq.numpy(), k.numpy(), v.numpy(),
+                                         attn_mask=m.numpy(), return_f32=True)
+        assert_parity(o, expect, f"strided key mask nq={nq}")
+
+
+KEY_BYTE_CASES = [
+    # B, Hq, Hkv, Nq, Nk, D, causal, bf16, batch-broadcast, key stride
+    (4, 32, 8, 1, 8192, 128, 0, False, False, 1),   # decode, splits + combine
+    (2, 14, 2, 1, 3001, 64, 0, True, False, 1),     # Qwen2-0.5B heads, bf16
+    (3, 8, 8, 2, 77, 64, 1, False, True, 1),        # top-left decode, broadcast batch
+    (1, 4, 4, 512, 512, 128, 0, False, False, 3),   # small launch, strided key bytes
+    (2, 8, 2, 300, 700, 128, 2, False, False, 1),   # prefill kernel, bottom-right
+    (1, 8, 2, 1000, 1000, 64, 1, True, False, 2),   # prefill, bf16, causal
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Nq,Nk,D,causal,bf16,bcast,sk", KEY_BYTE_CASES)
+def test_key_bytes_equal_packed_bits(device, B, Hq, Hkv, Nq, Nk, D, causal, bf16, bcast, sk):
+    """Through the C ABI: a key-padding mask given as bytes (mask_keys, read
+    in place) and the same mask packed into bit rows (mask_bits) give the
+    same O and LSE bit for bit, with and without a split-K workspace."""
+    from capi_types import Params
+    print(f"[key bytes] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} causal={causal} "
+          f"bf16={bf16} bcast={bcast} sk={sk}", flush=True)
+    lib = ctypes.CDLL(LIB)
+    lib.fa_sm75_forward.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_workspace_size.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_workspace_size.restype = ctypes.c_int64
+    lib.fa_sm75_set_contiguous_strides.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_last_error.restype = ctypes.c_char_p
+    pack = lib.fa_sm75_pack_mask
+    pack.argtypes = [ctypes.c_void_p] + [ctypes.c_int64] * 8 + [ctypes.c_void_p, ctypes.c_void_p]
+    dt = torch.bfloat16 if bf16 else torch.float16
+    g = torch.Generator("cpu").manual_seed(B * 1000 + Nk)
+    q = torch.randn(B, Hq, Nq, D, generator=g).to(dt).to(device)
+    k = torch.randn(B, Hkv, Nk, D, generator=g).to(dt).to(device)
+    v = torch.randn(B, Hkv, Nk, D, generator=g).to(dt).to(device)
+    mb = 1 if bcast else B
+    keys = (torch.rand(mb, Nk * sk, generator=g) < 0.7).to(device)  # [mb, Nk*sk] bytes
+    keys[:, 0] = True
+    kview = keys[:, ::sk]
+    words = (Nk + 63) // 64
+    bits = torch.empty(mb, 1, 1, words, dtype=torch.int64, device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert pack(kview.data_ptr(), mb, 1, 1, Nk, kview.stride(0), 0, 0, kview.stride(1),
+                bits.data_ptr(), stream) == 0
+
+    def run(use_bytes, with_ws):
+        o = torch.full_like(q, float("nan"))
+        lse = torch.full((B, Hq, Nq), float("nan"), device=device)
+        p = Params()
+        p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr()
+        p.batch, p.heads_q, p.heads_kv, p.seq_len, p.head_dim = B, Hq, Hkv, Nq, D
+        p.seq_len_kv = Nk
+        lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+        p.scale, p.causal, p.dtype = D ** -0.5, causal, 1 if bf16 else 0
+        p.stream = stream
+        if use_bytes:
+            p.mask_keys = kview.data_ptr()
+            p.mask_keys_stride_b = kview.stride(0) if mb > 1 else 0
+            p.mask_keys_stride_k = kview.stride(1)
+        else:
+            p.mask_bits = bits.data_ptr()
+            p.mask_stride_b = words if mb > 1 else 0
+        ws = None
+        if with_ws:
+            n = lib.fa_sm75_workspace_size(ctypes.byref(p))
+            if n > 0:
+                ws = torch.empty(n, dtype=torch.uint8, device=device)
+                p.workspace, p.workspace_bytes = ws.data_ptr(), n
+        assert lib.fa_sm75_forward(ctypes.byref(p)) == 0, lib.fa_sm75_last_error()
+        torch.cuda.synchronize()
+        return o, lse
+
+    for with_ws in (True, False):
+        ob, lb = run(True, with_ws)
+        op, lp = run(False, with_ws)
+        assert torch.equal(ob, op), f"O differs (workspace={with_ws})"
+        assert torch.equal(lb, lp), f"LSE differs (workspace={with_ws})"
+    npf = lambda t: t.float().cpu().numpy()
+    m_np = kview.cpu().numpy()[:, None, None, :]
+    if bf16:
+        want = ref.attention_f64(npf(q), npf(k), npf(v), causal=causal, attn_mask=m_np)
+        spv = ref.attention_f64(npf(q), npf(k), np.abs(npf(v)), causal=causal, attn_mask=m_np)
+        bound = 2.0 ** -8 * (spv + 2 * np.abs(want)) * 1.01 + 2e-6
+        assert np.all(np.abs(npf(ob) - want) <= bound)
+    else:
+        want = ref.attention_reference(npf(q), npf(k), npf(v), causal=causal, attn_mask=m_np,
+                                       return_f32=True)
+        assert_parity(ob, want, "key bytes")
