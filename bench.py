@@ -40,7 +40,8 @@ those calls over its wall time.  Besides the driver's keys the line holds
   widened       the calls beyond the reference's fp16 square launches on the
                 C4 shape: bfloat16 forward and backward, a key-padding boolean
                 mask, and a chunked prefill (Nq=2048 against Nk=8192,
-                bottom-right causal): average call time and TFLOPS.
+                bottom-right causal): average call time and TFLOPS; and a
+                padded-batch decode (D3 with a key-padding mask): GB/s.
 Diagnostics go to stderr.
 """
 import argparse
@@ -434,8 +435,9 @@ def time_calls(fn, steps=20, warm_ms=100.0):
 def time_widened(steps=20):
     """The calls the hot path was widened to, beyond the reference's fp16
     square launches: bfloat16 forward and backward on the C4 shape, C4 with a
-    key-padding boolean mask (the masked kernel), and a chunked prefill
-    (2048 new rows against 8192 cached keys, bottom-right causal)."""
+    key-padding boolean mask (the masked kernel), a padded-batch decode (D3
+    with a key-padding mask) and a chunked prefill (2048 new rows against
+    8192 cached keys, bottom-right causal)."""
     import torch
 
     from flash_attention_sm75 import flash_attention_forward_ex
@@ -465,6 +467,24 @@ def time_widened(steps=20):
     out["mask_fwd"] = {"workload": "C4 shape, causal and a [B,1,1,N] key-padding mask "
                                    "(last 10% hidden); FLOPs counted as unmasked causal",
                        "ms": round(ms, 5), "tflops": round(F / (ms * 1e-3) / 1e12, 1)}
+
+    # Padded-batch decode: D3's shape, each sequence of the batch a different
+    # length (a [B,1,1,Nk] key-padding mask, read in place as bytes).
+    Bd, Hqd, Hkvd, Nqd, Nkd, Dd = DECODE_CONFIGS["D3"]
+    qd = torch.randn(Bd, Hqd, Nqd, Dd, generator=g).half().to(dev)
+    kd = torch.randn(Bd, Hkvd, Nkd, Dd, generator=g).half().to(dev)
+    vd = torch.randn(Bd, Hkvd, Nkd, Dd, generator=g).half().to(dev)
+    lens = torch.linspace(Nkd // 2, Nkd, Bd).long().to(dev)
+    pad = (torch.arange(Nkd, device=dev)[None, :] < lens[:, None])[:, None, None, :]
+    ms = time_calls(lambda: flash_attention_forward_ex(qd, kd, vd, attn_mask=pad), steps)
+    nbytes = 2 * Bd * Hkvd * Nkd * Dd * 2 + 2 * Bd * Hqd * Nqd * Dd * 2
+    out["mask_decode"] = {"workload": f"decode B={Bd} Hq={Hqd} Hkv={Hkvd} Nq={Nqd} Nk={Nkd} "
+                                      f"d={Dd}, [B,1,1,Nk] key-padding mask (lengths "
+                                      f"{Nkd // 2}..{Nkd})",
+                          "ms": round(ms, 5),
+                          "gb_per_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                          "bytes": "all of K and V counted (the kernel reads every tile)"}
+    del qd, kd, vd
 
     nq = 2048
     qc = q[:, :, N - nq:].contiguous()
