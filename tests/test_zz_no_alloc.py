@@ -5,7 +5,8 @@ Checked through the C ABI against fa_sm75_forward given a workspace of
 fa_sm75_workspace_size() bytes: bitwise equal outputs and LSE, on two calls
 in a row where the second is smaller (the scratch keeps the first call's
 contents), for the two paths that use scratch: the split-K decode kernel
-(partials) and the fused kernel's dynamic schedule (queue counters).
+(partials; also with a key-padding mask read as bytes) and the fused
+kernel's dynamic schedule (queue counters).
 """
 import ctypes
 
@@ -35,15 +36,17 @@ def lib():
     return lib
 
 
-def call_pair(lib, device, B, Hq, Hkv, Nq, Nk, D, causal, seed):
+def call_pair(lib, device, B, Hq, Hkv, Nq, Nk, D, causal, seed, key_mask=False):
     """Runs one problem through both entry points; returns the two (O, LSE)
-    pairs and the workspace size the call asks for."""
-    print(f"[noalloc] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} causal={causal}",
-          flush=True)
+    pairs and the workspace size the call asks for.  key_mask: a random
+    [B, Nk] key-padding mask given as bytes (mask_keys)."""
+    print(f"[noalloc] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} causal={causal} "
+          f"key_mask={key_mask}", flush=True)
     g = torch.Generator("cpu").manual_seed(seed)
     q = torch.randn(B, Hq, Nq, D, generator=g).half().to(device)
     k = torch.randn(B, Hkv, Nk, D, generator=g).half().to(device)
     v = torch.randn(B, Hkv, Nk, D, generator=g).half().to(device)
+    keys = (torch.rand(B, Nk, generator=g) < 0.8).to(device) if key_mask else None
     outs = []
     need = None
     for entry in ("fa_sm75_forward", "fa_sm75_forward_noalloc"):
@@ -57,6 +60,8 @@ def call_pair(lib, device, B, Hq, Hkv, Nq, Nk, D, causal, seed):
         lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
         p.scale, p.causal = D ** -0.5, causal
         p.stream = torch.cuda.current_stream().cuda_stream
+        if keys is not None:
+            p.mask_keys, p.mask_keys_stride_b, p.mask_keys_stride_k = keys.data_ptr(), Nk, 1
         ws = None
         if entry == "fa_sm75_forward":
             need = lib.fa_sm75_workspace_size(ctypes.byref(p))
@@ -83,6 +88,16 @@ def test_split_k_partials_in_scratch(device, lib):
     assert need > 0
     assert_same(outs)
     outs, need2 = call_pair(lib, device, 1, 8, 2, 3, 700, 64, 2, seed=2)  # smaller
+    assert 0 < need2 < need
+    assert_same(outs)
+
+
+def test_split_k_with_key_padding_mask(device, lib):
+    # the same, with a key-padding mask read as bytes
+    outs, need = call_pair(lib, device, 4, 14, 2, 1, 6000, 64, 0, seed=5, key_mask=True)
+    assert need > 0
+    assert_same(outs)
+    outs, need2 = call_pair(lib, device, 2, 8, 2, 1, 1500, 128, 2, seed=6, key_mask=True)
     assert 0 < need2 < need
     assert_same(outs)
 
