@@ -41,7 +41,7 @@ those calls over its wall time.  Besides the driver's keys the line holds
                 C4 shape: bfloat16 forward and backward, a key-padding boolean
                 mask, and a chunked prefill (Nq=2048 against Nk=8192,
                 bottom-right causal): average call time and TFLOPS; and a
-                padded-batch decode (D3 with a key-padding mask): GB/s.
+                padded-batch decode (D1 with a key-padding mask): GB/s.
 Diagnostics go to stderr.
 """
 import argparse
@@ -435,7 +435,7 @@ def time_calls(fn, steps=20, warm_ms=100.0):
 def time_widened(steps=20):
     """The calls the hot path was widened to, beyond the reference's fp16
     square launches: bfloat16 forward and backward on the C4 shape, C4 with a
-    key-padding boolean mask (the masked kernel), a padded-batch decode (D3
+    key-padding boolean mask (the masked kernel), a padded-batch decode (D1
     with a key-padding mask) and a chunked prefill (2048 new rows against
     8192 cached keys, bottom-right causal)."""
     import torch
@@ -468,22 +468,29 @@ def time_widened(steps=20):
                                    "(last 10% hidden); FLOPs counted as unmasked causal",
                        "ms": round(ms, 5), "tflops": round(F / (ms * 1e-3) / 1e12, 1)}
 
-    # Padded-batch decode: D3's shape, each sequence of the batch a different
-    # length (a [B,1,1,Nk] key-padding mask, read in place as bytes).
-    Bd, Hqd, Hkvd, Nqd, Nkd, Dd = DECODE_CONFIGS["D3"]
+    # Padded-batch decode: D1's shape (a batched Llama-style decode step), the
+    # sequences of the batch of lengths Nk/2 .. Nk (a [B,1,1,Nk] key-padding
+    # mask, read in place as bytes; tiles no row sees are not read).
+    Bd, Hqd, Hkvd, Nqd, Nkd, Dd = DECODE_CONFIGS["D1"]
     qd = torch.randn(Bd, Hqd, Nqd, Dd, generator=g).half().to(dev)
     kd = torch.randn(Bd, Hkvd, Nkd, Dd, generator=g).half().to(dev)
     vd = torch.randn(Bd, Hkvd, Nkd, Dd, generator=g).half().to(dev)
     lens = torch.linspace(Nkd // 2, Nkd, Bd).long().to(dev)
     pad = (torch.arange(Nkd, device=dev)[None, :] < lens[:, None])[:, None, None, :]
     ms = time_calls(lambda: flash_attention_forward_ex(qd, kd, vd, attn_mask=pad), steps)
-    nbytes = 2 * Bd * Hkvd * Nkd * Dd * 2 + 2 * Bd * Hqd * Nqd * Dd * 2
+    # Bytes the call needs: K and V of the 32-key tiles that hold a visible
+    # key, Q and O; nominal: all of K and V.
+    tiles = sum(-(-int(n) // 32) for n in lens.tolist())
+    nbytes = 2 * Hkvd * min(tiles * 32, Bd * Nkd) * Dd * 2 + 2 * Bd * Hqd * Nqd * Dd * 2
+    nominal = 2 * Bd * Hkvd * Nkd * Dd * 2 + 2 * Bd * Hqd * Nqd * Dd * 2
     out["mask_decode"] = {"workload": f"decode B={Bd} Hq={Hqd} Hkv={Hkvd} Nq={Nqd} Nk={Nkd} "
                                       f"d={Dd}, [B,1,1,Nk] key-padding mask (lengths "
                                       f"{Nkd // 2}..{Nkd})",
                           "ms": round(ms, 5),
                           "gb_per_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                          "bytes": "all of K and V counted (the kernel reads every tile)"}
+                          "nominal_gb_per_s": round(nominal / (ms * 1e-3) / 1e9, 1),
+                          "bytes": "gb_per_s: K and V of the tiles holding a visible key, Q, O "
+                                   "(the padding's tiles are not read); nominal: all of K and V"}
     del qd, kd, vd
 
     nq = 2048

@@ -254,13 +254,33 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
 
   half8 kA[KK], kB[KK];
 
+  // The word of a tile from what load_mask returned (bit k: key 32 t + k
+  // visible): key bytes (lanes l and l + 32 hold key 32 t + l) give it as the
+  // low half of a ballot; mask bits are the lane's word itself.
+  auto word_of = [&](uint32_t raw) -> uint32_t {
+    if constexpr (KEY_BYTES) return (uint32_t)__builtin_amdgcn_ballot_w64(raw != 0);
+    else return raw;
+  };
+  // Whether no lane (query row) sees a key of a tile: its K and V are then
+  // not read (an empty window: zeros, no memory traffic) and its scores are
+  // all masked, so it adds exactly nothing.  Padded batches skip their
+  // padding this way.
+  auto hidden = [&](uint32_t w) -> bool { return __builtin_amdgcn_ballot_w64(w != 0) == 0; };
+
   // One tile: S, softmax, P V.  The loads of the next tile are issued first.
+  // MASK: mw and w_next are the words of tiles it and it + 1; raw2 is what
+  // load_mask returned for tile it + 2 (issued a step ago), and tile it + 3's
+  // mask load goes to raw3.  Returns tile it + 2's word, formed after this
+  // step's V wait, when raw2 has landed: every mask load is issued two steps
+  // before its tile's K and V loads, so deciding whether they are needed
+  // never waits.
   auto step = [&](int it, half8 (&kc)[KK], half8 (&kn)[KK], _Float16* vc, _Float16* vn,
-                  uint32_t mw, uint32_t& mw_next) {
+                  uint32_t mw, uint32_t w_next, uint32_t raw2, uint32_t& raw3) -> uint32_t {
     const bool has_next = it + 1 < nt_w;
-    if (MASK) mw_next = load_mask(it + 1, has_next);
-    load_k(it + 1, kn, has_next);
-    load_v(it + 1, vn, has_next);
+    const bool skip_next = MASK && hidden(w_next);
+    if (MASK) raw3 = load_mask(it + 3, it + 3 < nt_w);
+    load_k(it + 1, kn, has_next && !skip_next);
+    load_v(it + 1, vn, has_next && !skip_next);
     float16v s = (float16v)0.0f;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
@@ -269,10 +289,6 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     const int kstart = key0 + (wave + kWaves * it) * kDecTile;
     bool need_mask =
         (kstart + kDecTile > NK) || (CAUSAL && kstart + kDecTile - 1 > qi_lo + a.diag);
-    // Key bytes: lanes l and l + 32 hold key kstart + l, so the low half of
-    // the ballot is the tile's word (read here, after the next tile's loads
-    // are issued, as the word itself is).
-    if constexpr (KEY_BYTES) mw = (uint32_t)__builtin_amdgcn_ballot_w64(mw != 0);
     if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
     if (need_mask) {
       const uint32_t mws = mw >> (4 * hi);  // bit 8 (i / 4) + i % 4: element i
@@ -312,6 +328,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     // V of this tile has landed once only the next tile's loads are pending
     // (loads complete in order).
     wait_vmcnt<KK + SEGS + (MASK ? 1 : 0)>();
+    const uint32_t w_next2 = MASK ? word_of(raw2) : ~0u;
     half8 vf[NPV];
 #pragma unroll
     for (int v = 0; v < NPV; ++v) vf[v] = read_v(vc, v);
@@ -320,19 +337,35 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
       const int ks = v / MT, mt = v % MT;
       oacc[mt] = E::mfma(vf[v], __builtin_bit_cast(half8, pf[ks]), oacc[mt]);
     }
+    return w_next2;
   };
 
   if (nt_w > 0) {
-    uint32_t mwA = ~0u, mwB = ~0u;
-    if (MASK) mwA = load_mask(0, true);
+    // Every step issues one mask load (MASK), then K and V of its next tile;
+    // the prologue issues the masks of tiles 0, 1 and 2, then K and V of tile
+    // 0 (read whether hidden or not: deciding would wait for its mask first).
+    uint32_t raw0 = 0u, raw1 = 0u, rawA = 0u, rawB = 0u, wc = ~0u, wn = ~0u;
+    if (MASK) {
+      raw0 = load_mask(0, true);
+      raw1 = load_mask(1, 1 < nt_w);
+      rawB = load_mask(2, 2 < nt_w);
+    }
     load_k(0, kA, true);
     load_v(0, my_v0, true);
+    if (MASK) {
+      wc = word_of(raw0);
+      wn = word_of(raw1);
+    }
     int it = 0;
     for (; it + 1 < nt_w; it += 2) {
-      step(it, kA, kB, my_v0, my_v1, mwA, mwB);
-      step(it + 1, kB, kA, my_v1, my_v0, mwB, mwA);
+      uint32_t w2 = step(it, kA, kB, my_v0, my_v1, wc, wn, rawB, rawA);
+      wc = wn;
+      wn = w2;
+      w2 = step(it + 1, kB, kA, my_v1, my_v0, wc, wn, rawA, rawB);
+      wc = wn;
+      wn = w2;
     }
-    if (it < nt_w) step(it, kA, kB, my_v0, my_v1, mwA, mwB);
+    if (it < nt_w) step(it, kA, kB, my_v0, my_v1, wc, wn, rawB, rawA);
   }
 
   // ---- merge the four waves through LDS (the V tiles are free now) --------

@@ -290,3 +290,67 @@ def test_key_bytes_equal_packed_bits(device, B, Hq, Hkv, Nq, Nk, D, causal, bf16
         want = ref.attention_reference(npf(q), npf(k), npf(v), causal=causal, attn_mask=m_np,
                                        return_f32=True)
         assert_parity(ob, want, "key bytes")
+
+
+PADDING_CASES = [
+    # B, Hq, Hkv, Nq, Nk, D, bf16, per-row (packed bits) instead of key bytes
+    (6, 14, 2, 1, 9000, 64, False, False),   # decode, splits + combine
+    (5, 32, 8, 1, 4100, 128, True, False),   # bf16
+    (4, 8, 2, 4, 3000, 128, False, True),    # 16 rows per unit, packed per-row words
+    (3, 4, 4, 300, 1500, 64, False, False),  # small launch (row blocks of 32)
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Nq,Nk,D,bf16,per_row", PADDING_CASES)
+def test_padding_layouts_skip_hidden_tiles(device, B, Hq, Hkv, Nq, Nk, D, bf16, per_row):
+    """The split-K kernel does not read K/V tiles that no query row of a
+    workgroup sees (a padded batch's padding).  Contiguous padding hides
+    whole 32-key tiles: right padding, left padding, a hole, a sequence with
+    every key hidden (O = 0, LSE = -inf) and one that sees only its last key,
+    one per batch entry; against the oracle incl. LSE."""
+    print(f"[padding] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} bf16={bf16} per_row={per_row}",
+          flush=True)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    g = torch.Generator("cpu").manual_seed(Nk + B)
+    q = torch.randn(B, Hq, Nq, D, generator=g).to(dt)
+    k = torch.randn(B, Hkv, Nk, D, generator=g).to(dt)
+    v = torch.randn(B, Hkv, Nk, D, generator=g).to(dt)
+    keys = torch.zeros(B, Nk, dtype=torch.bool)
+    layouts = [(0, Nk // 3), (Nk - Nk // 5, Nk), (0, Nk)]  # right pad, left pad, full
+    for b in range(B):
+        kind = b % 6
+        if kind < 3:
+            lo, hi = layouts[kind]
+            keys[b, lo:hi] = True
+        elif kind == 3:  # a hole in the middle
+            keys[b] = True
+            keys[b, Nk // 4: Nk // 2] = False
+        elif kind == 4:  # every key hidden
+            pass
+        else:  # only the last key
+            keys[b, Nk - 1] = True
+    m = keys[:, None, None, :]
+    if per_row:
+        m = m.expand(B, Hq, Nq, Nk).contiguous()
+    o, lse = flash_attention_forward_ex(q.to(device), k.to(device), v.to(device),
+                                        return_lse=True, attn_mask=m.to(device))
+    torch.cuda.synchronize()
+    npf = lambda t: t.float().numpy()
+    m_np = np.broadcast_to(m.numpy(), (B, Hq, Nq, Nk))
+    got = o.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    if bf16:
+        want = ref.attention_f64(npf(q), npf(k), npf(v), attn_mask=m_np)
+        spv = ref.attention_f64(npf(q), npf(k), np.abs(npf(v)), attn_mask=m_np)
+        assert np.all(np.abs(got - want) <= 2.0 ** -8 * (spv + 2 * np.abs(want)) * 1.01 + 2e-6)
+    else:
+        want = ref.attention_reference(npf(q), npf(k), npf(v), attn_mask=m_np, return_f32=True)
+        assert_parity(o, want, "padding")
+    if B > 4:
+        assert np.all(got[4] == 0)  # the sequence that sees no key
+    wl = ref.attention_lse(npf(q), npf(k), attn_mask=m_np)
+    gl = lse.cpu().numpy()
+    fin = np.isfinite(wl)
+    assert np.array_equal(np.isfinite(gl), fin)
+    tol = float(np.log1p(2.0 ** -8)) + 1e-5 if bf16 else 1e-3
+    np.testing.assert_allclose(gl[fin], wl[fin], atol=tol, rtol=0 if bf16 else 1e-4)
