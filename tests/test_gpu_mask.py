@@ -67,6 +67,33 @@ def test_pack_mask_bits(device):
     assert np.array_equal(out2.cpu().numpy().view(np.uint64), want)
 
 
+@pytest.mark.parametrize("nk,off", [(1, 0), (17, 5), (1000, 3), (1024, 0), (1025, 7), (2049, 3),
+                                    (4097, 0), (5000, 5)])
+def test_pack_mask_rows_unaligned(device, nk, off):
+    """Rows of consecutive bytes at any alignment and length (16-byte loads,
+    one or two 1024-byte chunks per pass, the row's last partial 16 bytes one
+    by one) against numpy."""
+    lib = ctypes.CDLL(LIB)
+    f = lib.fa_sm75_pack_mask
+    f.argtypes = [ctypes.c_void_p] + [ctypes.c_int64] * 8 + [ctypes.c_void_p, ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    B, Nq = 2, 3
+    g = torch.Generator("cpu").manual_seed(nk + off)
+    base = torch.rand(B * Nq * nk + off + 16, generator=g) < 0.5
+    m = base[off:off + B * Nq * nk].view(B, 1, Nq, nk)
+    md = base.to(device)[off:off + B * Nq * nk].view(B, 1, Nq, nk)
+    words = (nk + 63) // 64
+    out = torch.full((B, 1, Nq, words), -1, dtype=torch.int64, device=device)
+    st = md.stride()
+    assert f(md.data_ptr(), B, 1, Nq, nk, st[0], 0, st[2], st[3], out.data_ptr(),
+             torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    padded = np.zeros((B, 1, Nq, words * 64), dtype=np.uint8)
+    padded[..., :nk] = m.numpy()
+    want = np.packbits(padded.reshape(B, 1, Nq, words, 64), axis=-1, bitorder="little")
+    assert np.array_equal(out.cpu().numpy().view(np.uint64), want.view(np.uint64).reshape(out.shape))
+
+
 CASES = [
     # B, Hq, Hkv, Nq, Nk, D, mask shape (broadcast), p(visible), causal
     (2, 4, 2, 300, 300, 128, (2, 4, 300, 300), 0.6, False),
