@@ -99,6 +99,15 @@ int validate(const fa_fwd_params* p, bool fused) {
                   "mask row stride %lld is below ceil(seq_len_kv / 64) = %lld words",
                   (long long)p->mask_stride_q, (long long)((kv_rows(p) + 63) / 64));
   }
+  if (p->mask_ranges != nullptr) {
+    if (p->mask_bits == nullptr)
+      return fail(FA_ERR_INVALID_ARGUMENT, "mask_ranges needs mask_bits");
+    if ((reinterpret_cast<uintptr_t>(p->mask_ranges) & 7u) != 0)
+      return fail(FA_ERR_MISALIGNED, "mask_ranges must be 8-byte aligned");
+    if (p->mask_ranges_stride_b < 0 || p->mask_ranges_stride_h < 0 ||
+        p->mask_ranges_stride_q < 0)
+      return fail(FA_ERR_INVALID_ARGUMENT, "mask_ranges strides must be non-negative");
+  }
   if (p->mask_keys != nullptr) {
     if (!fused)
       return fail(FA_ERR_INVALID_ARGUMENT, "the naive path takes no mask");
@@ -173,6 +182,10 @@ fa::FwdArgs make_args(const fa_fwd_params* p) {
   a.mkeys = p->mask_keys;
   a.mksb = p->mask_keys_stride_b;
   a.mksk = p->mask_keys_stride_k;
+  a.mranges = p->mask_ranges;
+  a.mrsb = p->mask_ranges_stride_b;
+  a.mrsh = p->mask_ranges_stride_h;
+  a.mrsq = p->mask_ranges_stride_q;
   a.ctr = nullptr;
   a.items = 0;
   a.bf16 = p->dtype == FA_DTYPE_BF16 ? 1 : 0;
@@ -430,22 +443,50 @@ int fa_sm75_forward_noalloc(const fa_fwd_params* p) {
   return fa_sm75_forward(&q);
 }
 
-int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
-                      int64_t cols, int64_t stride_b, int64_t stride_h, int64_t stride_q,
-                      int64_t stride_k, uint64_t* out, void* stream) {
+namespace {
+
+int pack_mask_impl(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows, int64_t cols,
+                   int64_t stride_b, int64_t stride_h, int64_t stride_q, int64_t stride_k,
+                   uint64_t* out, int32_t* ranges, void* stream) {
   g_last_error[0] = '\0';
   if (batch < 0 || heads < 0 || rows < 0 || cols < 0)
     return fail(FA_ERR_INVALID_ARGUMENT, "mask sizes must be non-negative");
   if (stride_b < 0 || stride_h < 0 || stride_q < 0 || stride_k < 0)
     return fail(FA_ERR_INVALID_ARGUMENT, "mask strides must be non-negative");
+  if (cols > INT32_MAX / 2)
+    return fail(FA_ERR_TOO_LARGE, "mask cols %lld exceeds the supported maximum",
+                (long long)cols);
   if (batch == 0 || heads == 0 || rows == 0 || cols == 0) return FA_OK;
   if (mask == nullptr || out == nullptr)
     return fail(FA_ERR_INVALID_ARGUMENT, "mask and out must not be NULL");
   if ((reinterpret_cast<uintptr_t>(out) & 7u) != 0)
     return fail(FA_ERR_MISALIGNED, "out must be 8-byte aligned");
+  if (ranges != nullptr && (reinterpret_cast<uintptr_t>(ranges) & 7u) != 0)
+    return fail(FA_ERR_MISALIGNED, "ranges must be 8-byte aligned");
   fa::launch_pack_mask(mask, batch, heads, rows, cols, stride_b, stride_h, stride_q, stride_k,
-                       out, reinterpret_cast<hipStream_t>(stream));
+                       out, ranges, reinterpret_cast<hipStream_t>(stream));
   return check_launch();
+}
+
+}  // namespace
+
+int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
+                      int64_t cols, int64_t stride_b, int64_t stride_h, int64_t stride_q,
+                      int64_t stride_k, uint64_t* out, void* stream) {
+  return pack_mask_impl(mask, batch, heads, rows, cols, stride_b, stride_h, stride_q, stride_k,
+                        out, nullptr, stream);
+}
+
+int fa_sm75_pack_mask_ranges(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
+                             int64_t cols, int64_t stride_b, int64_t stride_h,
+                             int64_t stride_q, int64_t stride_k, uint64_t* out,
+                             int32_t* ranges, void* stream) {
+  if (ranges == nullptr) {
+    g_last_error[0] = '\0';
+    return fail(FA_ERR_INVALID_ARGUMENT, "ranges must not be NULL");
+  }
+  return pack_mask_impl(mask, batch, heads, rows, cols, stride_b, stride_h, stride_q, stride_k,
+                        out, ranges, stream);
 }
 
 int fa_sm75_set_kernel_policy(int policy) {

@@ -264,14 +264,48 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       for (int kk = 0; kk < KK; ++kk) qf[kk] = negate16(qf[kk]);
     }
 
+    // Mask ranges (mask bits with a.mranges): the span of keys some row of
+    // the block sees, [span_lo, span_hi); the tiles outside it hide every
+    // key from every row, so skipping them changes no result.  Each lane
+    // reads its row's pair (rows past N read row N - 1), the wave and then
+    // the workgroup (through V_1's buffer, which no load writes before step
+    // 0) take the union.
+    int span_lo = 0, span_hi = NK;
+    if constexpr (MASK && !KEY_BYTES) {
+      if (a.mranges != nullptr) {
+        const int32_t* rr =
+            a.mranges + 2 * (b * a.mrsb + hq * a.mrsh + (int64_t)min(qrow, N - 1) * a.mrsq);
+        span_lo = rr[0];
+        span_hi = rr[1];
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          span_lo = min(span_lo, __shfl_xor(span_lo, d));
+          span_hi = max(span_hi, __shfl_xor(span_hi, d));
+        }
+        int* const xs = (int*)v_lds1 + 16;
+        if (lane == 0) {
+          xs[2 * wave] = span_lo;
+          xs[2 * wave + 1] = span_hi;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+          span_lo = min(span_lo, xs[2 * w]);
+          span_hi = max(span_hi, xs[2 * w + 1]);
+        }
+        span_lo = __builtin_amdgcn_readfirstlane(span_lo);
+        span_hi = __builtin_amdgcn_readfirstlane(span_hi);
+      }
+    }
     // Keys this block can see (none for a block entirely before the diagonal).
-    const int kv_len = CAUSAL ? max(0, min(NK, q0 + BLOCK_M + a.diag)) : NK;
+    const int kv_len = min(CAUSAL ? max(0, min(NK, q0 + BLOCK_M + a.diag)) : NK, span_hi);
     const int block_tiles = (kv_len + kBlockN - 1) / kBlockN;
+    const int first_tile = span_lo < span_hi ? span_lo / kBlockN : 0;
     // Tiles [tile0, tile0 + ntiles) of this wave's key group.  KSPLIT: both
     // groups run ceil(block_tiles / 2) steps (so their barriers pair up); a
     // tile past the block's keys is fully masked and adds exactly nothing.
-    const int ntiles = KSPLIT ? (block_tiles + 1) / 2 : block_tiles;
-    const int tile0 = KSPLIT ? kgrp * ntiles : 0;
+    const int ntiles = KSPLIT ? (block_tiles + 1) / 2 : max(0, block_tiles - first_tile);
+    const int tile0 = KSPLIT ? kgrp * ntiles : first_tile;
     const int tile_end = tile0 + ntiles;
 
     // Direct-load map: wave quarter wq fills 1 KB segments wq, wq + 4, ... of a

@@ -35,6 +35,8 @@ struct FwdArgs {
   int64_t msb, msh, msq;   // its strides in 64-bit words
   const uint8_t* mkeys;    // key-padding mask bytes or nullptr (fa_fwd_params.mask_keys);
   int64_t mksb, mksk;      //   exclusive with mbits; its batch and key strides in bytes
+  const int32_t* mranges;  // per mask row (first, one past last) visible key, or nullptr
+  int64_t mrsb, mrsh, mrsq;  // its strides in pairs (fa_fwd_params.mask_ranges)
   uint64_t* ctr;    // queue counters of the dynamic schedule, or nullptr (static)
   int items;        // work items (query blocks): filled by the launcher
   int bf16;         // elements are bfloat16 (else binary16)
@@ -186,10 +188,11 @@ int launch_backward(const BwdArgs& a, int batch, int head_dim, bool causal, bool
 template <int D, bool BF16, bool MASK>
 void launch_bwd(const BwdArgs& a, int batch, bool causal, hipStream_t stream);
 
-// Boolean mask -> bit rows (fa_mask.hip).
+// Boolean mask -> bit rows (fa_mask.hip); ranges (or nullptr): each row's
+// first visible key and one past the last ([cols, 0] for none), int32 pairs.
 int launch_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
                      int64_t cols, int64_t sb, int64_t sh, int64_t sq, int64_t sk,
-                     uint64_t* out, hipStream_t stream);
+                     uint64_t* out, int32_t* ranges, hipStream_t stream);
 
 // Three-kernel path through an fp32 [B*Hq, N, N] score workspace.
 int launch_naive_forward(const FwdArgs& a, int batch, int head_dim, bool causal,

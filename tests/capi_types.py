@@ -25,6 +25,8 @@ class Params(ctypes.Structure):
         ("dtype", ctypes.c_int),
         ("mask_keys", ctypes.c_void_p), ("mask_keys_stride_b", ctypes.c_int64),
         ("mask_keys_stride_k", ctypes.c_int64),
+        ("mask_ranges", ctypes.c_void_p), ("mask_ranges_stride_b", ctypes.c_int64),
+        ("mask_ranges_stride_h", ctypes.c_int64), ("mask_ranges_stride_q", ctypes.c_int64),
     ]]
 
 

@@ -241,8 +241,31 @@ def test_mask_keys_validation(lib):
     assert b"naive path takes no mask" in lib.fa_sm75_last_error()
 
 
+def test_mask_ranges_validation(lib):
+    """Row spans of visible keys: only with mask_bits, 8-byte aligned,
+    non-negative strides; the packing entry that writes them needs the
+    output (all rejected before any device work)."""
+    p = make(lib, mask_ranges=0x2000)
+    assert lib.fa_sm75_forward(ctypes.byref(p)) == 1
+    assert b"needs mask_bits" in lib.fa_sm75_last_error()
+    p = make(lib, mask_bits=0x1000, mask_ranges=0x2004)
+    assert lib.fa_sm75_forward(ctypes.byref(p)) == 4
+    assert b"8-byte aligned" in lib.fa_sm75_last_error()
+    for field in ("mask_ranges_stride_b", "mask_ranges_stride_h", "mask_ranges_stride_q"):
+        p = make(lib, mask_bits=0x1000, mask_ranges=0x2000, **{field: -1})
+        assert lib.fa_sm75_forward(ctypes.byref(p)) == 1
+        assert b"mask_ranges strides" in lib.fa_sm75_last_error()
+    f = lib.fa_sm75_pack_mask_ranges
+    f.argtypes = [ctypes.c_void_p] + [ctypes.c_int64] * 8 + [ctypes.c_void_p] * 3
+    f.restype = ctypes.c_int
+    assert f(0x1000, 1, 1, 1, 8, 0, 0, 0, 1, 0x1000, None, None) == 1
+    assert b"ranges must not be NULL" in lib.fa_sm75_last_error()
+    assert f(0x1000, 1, 1, 1, 8, 0, 0, 0, 1, 0x1000, 0x2004, None) == 4
+    assert f(0x1000, 1, 1, 1, 1 << 31, 0, 0, 0, 1, 0x1000, 0x2000, None) == 5
+
+
 def test_abi_version(lib):
-    assert lib.fa_sm75_abi_version() == 5
+    assert lib.fa_sm75_abi_version() == 6
 
 
 def test_kernel_policy_switch(lib):

@@ -381,3 +381,151 @@ def test_padding_layouts_skip_hidden_tiles(device, B, Hq, Hkv, Nq, Nk, D, bf16, 
     assert np.array_equal(np.isfinite(gl), fin)
     tol = float(np.log1p(2.0 ** -8)) + 1e-5 if bf16 else 1e-3
     np.testing.assert_allclose(gl[fin], wl[fin], atol=tol, rtol=0 if bf16 else 1e-4)
+
+
+def _pack_ranges_lib():
+    lib = ctypes.CDLL(LIB)
+    f = lib.fa_sm75_pack_mask_ranges
+    f.argtypes = [ctypes.c_void_p] + [ctypes.c_int64] * 8 + [ctypes.c_void_p] * 3
+    f.restype = ctypes.c_int
+    return lib
+
+
+@pytest.mark.parametrize("nk,sk", [(1, 1), (200, 1), (1500, 1), (2500, 1), (300, 3)])
+def test_pack_mask_ranges(device, nk, sk):
+    """Each row's first visible key and one past the last ([nk, 0] for a row
+    that sees none) next to the same bits as fa_sm75_pack_mask, for rows of
+    consecutive bytes and strided ones."""
+    lib = _pack_ranges_lib()
+    B, H, R = 2, 3, 5
+    g = torch.Generator("cpu").manual_seed(nk)
+    m = torch.zeros(B, H, R, nk * sk, dtype=torch.bool)
+    for b in range(B):
+        for h in range(H):
+            for r in range(R):
+                kind = (b * 15 + h * 5 + r) % 4
+                if kind == 0:  # empty row
+                    continue
+                lo = int(torch.randint(0, nk, (1,), generator=g))
+                hi = int(torch.randint(lo + 1, nk + 1, (1,), generator=g)) if kind != 3 else lo + 1
+                row = torch.rand(nk, generator=g) < 0.5
+                row[:lo] = False
+                row[hi:] = False
+                row[lo] = True
+                row[hi - 1] = True
+                m[b, h, r, ::sk] = row
+    mv = m[..., ::sk]
+    md = m.to(device)[..., ::sk]
+    words = (nk + 63) // 64
+    out = torch.full((B, H, R, words), -1, dtype=torch.int64, device=device)
+    ranges = torch.full((B, H, R, 2), -7, dtype=torch.int32, device=device)
+    st = md.stride()
+    assert lib.fa_sm75_pack_mask_ranges(md.data_ptr(), B, H, R, nk, st[0], st[1], st[2], st[3],
+                                        out.data_ptr(), ranges.data_ptr(),
+                                        torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    mn = mv.numpy()
+    padded = np.zeros((B, H, R, words * 64), dtype=np.uint8)
+    padded[..., :nk] = mn
+    want = np.packbits(padded.reshape(B, H, R, words, 64), axis=-1, bitorder="little")
+    assert np.array_equal(out.cpu().numpy().view(np.uint64), want.view(np.uint64).reshape(out.shape))
+    got = ranges.cpu().numpy()
+    for b in range(B):
+        for h in range(H):
+            for r in range(R):
+                idx = np.nonzero(mn[b, h, r])[0]
+                exp = (idx[0], idx[-1] + 1) if idx.size else (nk, 0)
+                assert tuple(got[b, h, r]) == exp, (b, h, r, tuple(got[b, h, r]), exp)
+
+
+RANGE_CASES = [
+    # B, Hq, Hkv, Nq, Nk, D, bf16, mask kind, policy
+    (2, 4, 2, 1000, 1000, 128, False, "causal+pad", 0),   # transformers' padded prefill
+    (3, 8, 2, 700, 700, 64, True, "causal+pad", 0),
+    (2, 4, 4, 300, 900, 64, False, "causal+pad", 0),       # Nq < Nk (chunked prefill with cache)
+    (2, 16, 4, 2048, 2048, 128, False, "causal+pad", 3),   # dynamic schedule: several items per WG
+    (2, 4, 2, 513, 513, 128, False, "per-head", 0),        # random per-head rows
+]
+
+
+def _range_mask(kind, B, Hq, Nq, Nk, g):
+    if kind == "per-head":
+        return torch.rand(B, Hq, Nq, Nk, generator=g) < 0.3
+    # causal (bottom-right for Nq < Nk) and left padding of B different lengths
+    i = torch.arange(Nq)[:, None] + (Nk - Nq)
+    j = torch.arange(Nk)[None, :]
+    m = (j <= i)[None, None].expand(B, 1, Nq, Nk).clone()
+    for b in range(B):
+        pad = (b * Nk) // (2 * B)
+        m[b, :, :, :pad] = False
+    return m
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Nq,Nk,D,bf16,kind,policy", RANGE_CASES)
+def test_mask_ranges_skip_tiles(device, B, Hq, Hkv, Nq, Nk, D, bf16, kind, policy):
+    """Through the C ABI: the same packed mask with and without mask_ranges
+    gives the same O and LSE bit for bit (the skipped tiles hide every key
+    from every row of their block), and the result meets the oracle's bar."""
+    from capi_types import Params
+    print(f"[ranges] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D} bf16={bf16} {kind} "
+          f"policy={policy}", flush=True)
+    lib = _pack_ranges_lib()
+    lib.fa_sm75_forward.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_workspace_size.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_workspace_size.restype = ctypes.c_int64
+    lib.fa_sm75_set_contiguous_strides.argtypes = [ctypes.POINTER(Params)]
+    lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
+    lib.fa_sm75_last_error.restype = ctypes.c_char_p
+    dt = torch.bfloat16 if bf16 else torch.float16
+    g = torch.Generator("cpu").manual_seed(Nq * 7 + Nk)
+    q = torch.randn(B, Hq, Nq, D, generator=g).to(dt).to(device)
+    k = torch.randn(B, Hkv, Nk, D, generator=g).to(dt).to(device)
+    v = torch.randn(B, Hkv, Nk, D, generator=g).to(dt).to(device)
+    m = _range_mask(kind, B, Hq, Nq, Nk, g)
+    md = m.to(device)
+    Hm = m.shape[1]
+    words = (Nk + 63) // 64
+    bits = torch.empty(B, Hm, Nq, words, dtype=torch.int64, device=device)
+    ranges = torch.empty(B, Hm, Nq, 2, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    st = md.stride()
+    assert lib.fa_sm75_pack_mask_ranges(md.data_ptr(), B, Hm, Nq, Nk, st[0], st[1], st[2], st[3],
+                                        bits.data_ptr(), ranges.data_ptr(), stream) == 0
+
+    def run(with_ranges):
+        o = torch.full_like(q, float("nan"))
+        lse = torch.full((B, Hq, Nq), float("nan"), device=device)
+        p = Params()
+        p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr()
+        p.batch, p.heads_q, p.heads_kv, p.seq_len, p.head_dim = B, Hq, Hkv, Nq, D
+        p.seq_len_kv = Nk
+        lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+        p.scale, p.dtype, p.stream = D ** -0.5, 1 if bf16 else 0, stream
+        p.mask_bits = bits.data_ptr()
+        p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = Hm * Nq * words, (Nq * words if Hm > 1 else 0), words
+        if with_ranges:
+            p.mask_ranges = ranges.data_ptr()
+            p.mask_ranges_stride_b, p.mask_ranges_stride_h, p.mask_ranges_stride_q = Hm * Nq, (Nq if Hm > 1 else 0), 1
+        n = lib.fa_sm75_workspace_size(ctypes.byref(p))
+        ws = torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+        p.workspace, p.workspace_bytes = ws.data_ptr(), n
+        assert lib.fa_sm75_forward(ctypes.byref(p)) == 0, lib.fa_sm75_last_error()
+        torch.cuda.synchronize()
+        return o, lse
+
+    assert lib.fa_sm75_set_kernel_policy(policy) == 0
+    try:
+        o1, l1 = run(True)
+        o0, l0 = run(False)
+    finally:
+        lib.fa_sm75_set_kernel_policy(0)
+    assert torch.equal(o1, o0) and torch.equal(l1, l0)
+    npf = lambda t: t.float().cpu().numpy()
+    mn = np.broadcast_to(m.numpy(), (B, Hq, Nq, Nk))
+    if bf16:
+        want = ref.attention_f64(npf(q), npf(k), npf(v), attn_mask=mn)
+        spv = ref.attention_f64(npf(q), npf(k), np.abs(npf(v)), attn_mask=mn)
+        assert np.all(np.abs(npf(o1) - want) <= 2.0 ** -8 * (spv + 2 * np.abs(want)) * 1.01 + 2e-6)
+    else:
+        want = ref.attention_reference(npf(q), npf(k), npf(v), attn_mask=mn, return_f32=True)
+        assert_parity(o1, want, "ranges")
