@@ -20,7 +20,6 @@
 
 #include <string>
 #include <tuple>
-#include <type_traits>
 
 #include "flash_attn_sm75.h"
 
@@ -167,13 +166,12 @@ int64_t eff_stride(const torch::Tensor& t, int i, int64_t fallback) {
 // Packs a boolean mask broadcastable to [B, Hq, Nq, Nk] into bit rows; the
 // mask's own size-1 (or stride-0) batch, head and query dimensions stay size
 // 1 in the packed tensor and get stride 0 in the params.  The forward
-// (fa_fwd_params) also gets each row's span of visible keys (mask_ranges),
-// one int64 per row after the words, so the fused kernel skips the tiles no
-// row of a block sees.
+// and the backward also get each row's span of visible keys (mask_ranges),
+// one int64 per row after the words, so the kernels skip the tiles no row
+// of a block sees.
 template <class Params>  // fa_fwd_params or fa_bwd_params (same mask fields)
 torch::Tensor pack_mask(const torch::Tensor& mask, const torch::Tensor& Q, int64_t nk,
                         Params& p) {
-  constexpr bool kRanges = std::is_same<Params, fa_fwd_params>::value;
   TORCH_CHECK(mask.dtype() == torch::kBool, "attn_mask must be a bool tensor");
   TORCH_CHECK(mask.device() == Q.device(), "attn_mask must be on Q's device");
   TORCH_CHECK(mask.dim() <= 4, "attn_mask must have at most 4 dimensions");
@@ -182,30 +180,24 @@ torch::Tensor pack_mask(const torch::Tensor& mask, const torch::Tensor& Q, int64
   for (int d = 0; d < 3; ++d) own[d] = (m.size(d) == 1 || m.stride(d) == 0) ? 1 : m.size(d);
   const int64_t words = (nk + 63) / 64;
   const int64_t nrows = own[0] * own[1] * own[2];
-  auto bits = torch::empty({nrows * (words + (kRanges ? 1 : 0))},
-                           Q.options().dtype(torch::kInt64));
+  auto bits = torch::empty({nrows * (words + 1)}, Q.options().dtype(torch::kInt64));
   uint64_t* const out = reinterpret_cast<uint64_t*>(bits.data_ptr<int64_t>());
-  int32_t* const ranges = kRanges ? reinterpret_cast<int32_t*>(out + nrows * words) : nullptr;
+  int32_t* const ranges = reinterpret_cast<int32_t*>(out + nrows * words);
   const auto* src = reinterpret_cast<const uint8_t*>(m.data_ptr<bool>());
   const int64_t sb = own[0] > 1 ? m.stride(0) : 0, sh = own[1] > 1 ? m.stride(1) : 0,
                 sq = own[2] > 1 ? m.stride(2) : 0;
   void* const stream = c10::hip::getCurrentHIPStream(Q.device().index()).stream();
-  const int st =
-      kRanges ? fa_sm75_pack_mask_ranges(src, own[0], own[1], own[2], nk, sb, sh, sq,
-                                         m.stride(3), out, ranges, stream)
-              : fa_sm75_pack_mask(src, own[0], own[1], own[2], nk, sb, sh, sq, m.stride(3), out,
-                                  stream);
+  const int st = fa_sm75_pack_mask_ranges(src, own[0], own[1], own[2], nk, sb, sh, sq,
+                                          m.stride(3), out, ranges, stream);
   TORCH_CHECK(st == FA_OK, "attn_mask packing: ", fa_sm75_last_error());
   p.mask_bits = out;
   p.mask_stride_b = own[0] > 1 ? own[1] * own[2] * words : 0;
   p.mask_stride_h = own[1] > 1 ? own[2] * words : 0;
   p.mask_stride_q = own[2] > 1 ? words : 0;
-  if constexpr (kRanges) {
-    p.mask_ranges = ranges;
-    p.mask_ranges_stride_b = own[0] > 1 ? own[1] * own[2] : 0;
-    p.mask_ranges_stride_h = own[1] > 1 ? own[2] : 0;
-    p.mask_ranges_stride_q = own[2] > 1 ? 1 : 0;
-  }
+  p.mask_ranges = ranges;
+  p.mask_ranges_stride_b = own[0] > 1 ? own[1] * own[2] : 0;
+  p.mask_ranges_stride_h = own[1] > 1 ? own[2] : 0;
+  p.mask_ranges_stride_q = own[2] > 1 ? 1 : 0;
   return bits;
 }
 

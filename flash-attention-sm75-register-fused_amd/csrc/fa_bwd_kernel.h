@@ -237,8 +237,54 @@ __global__ void __launch_bounds__(512, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = (float16v)0.0f;
 
-  const int qt_begin = CAUSAL ? min(a.qtiles, max(0, k0 - a.diag) / kBwdStatsTile) : 0;
-  const int per_head = a.qtiles - qt_begin;
+  // Mask ranges (a.mranges): the query rows whose span of visible keys
+  // meets this block's keys [k0, k0 + 128) (over the group's heads when the
+  // mask has a head dimension); the query tiles outside them see no key of
+  // the block, so skipping them changes no result.  Each thread scans a
+  // share of the rows, the wave and then the workgroup (through the P
+  // exchange buffers, idle until the first period) take the union.
+  int qt_lo = 0, qt_hi = a.qtiles;
+  if constexpr (MASK) {
+    if (a.mranges != nullptr) {
+      int lo = N, hi = 0;
+      const int heads = a.mrsh != 0 ? a.group : 1;
+      for (int r = (int)threadIdx.x; r < N; r += 512) {
+        for (int h = 0; h < heads; ++h) {
+          const int32_t* rr = a.mranges + 2 * (b * a.mrsb + (int64_t)(hkv * a.group + h) * a.mrsh +
+                                               (int64_t)r * a.mrsq);
+          if (rr[0] < k0 + kBwdBlockKeys && rr[1] > k0) {
+            lo = min(lo, r);
+            hi = max(hi, r + 1);
+          }
+        }
+      }
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        lo = min(lo, __shfl_xor(lo, d));
+        hi = max(hi, __shfl_xor(hi, d));
+      }
+      int* const xs = (int*)x_lds;
+      if (lane == 0) {
+        xs[2 * wave] = lo;
+        xs[2 * wave + 1] = hi;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int w2 = 0; w2 < 8; ++w2) {
+        lo = min(lo, xs[2 * w2]);
+        hi = max(hi, xs[2 * w2 + 1]);
+      }
+      __syncthreads();  // every wave has read the exchange before it is reused
+      lo = __builtin_amdgcn_readfirstlane(lo);
+      hi = __builtin_amdgcn_readfirstlane(hi);
+      qt_lo = hi > lo ? lo / kBwdStatsTile : 0;
+      qt_hi = hi > lo ? (hi + kBwdStatsTile - 1) / kBwdStatsTile : 0;
+    }
+  }
+  const int qt_begin =
+      max(qt_lo, CAUSAL ? min(a.qtiles, max(0, k0 - a.diag) / kBwdStatsTile) : 0);
+  const int qt_end = min(a.qtiles, qt_hi);
+  const int per_head = max(0, qt_end - qt_begin);
   const int steps = a.group * per_head;
 
   // P-waves load the Q tile, dS-waves the dO tile (segments kq, kq+4, ..).
@@ -506,8 +552,8 @@ __global__ void __launch_bounds__(512, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
   // that publishes it (and the P of step p); the roles run separate loops
   // with the same number of barriers.
   if (steps > 0) {
-    Cursor ic{a.qtiles - 1, 0};  // next step to load
-    Cursor wc{a.qtiles - 1, 0};  // step to work on
+    Cursor ic{qt_end - 1, 0};  // next step to load
+    Cursor wc{qt_end - 1, 0};  // step to work on
     issue(ic, I0{});
     advance(ic);
     barrier_after_loads<0>();
@@ -631,8 +677,39 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
 
   // dP accumulates onto -delta (every element of a lane is the lane's query).
   const float16v ndv = (float16v)ndelta;
-  const int kv_len = CAUSAL ? max(0, min(NK, q0 + kBwdBlockRows + a.diag)) : NK;
+  // Mask ranges (a.mranges): the span of keys some row of the block sees;
+  // the tiles outside it hide every key from every row (as in the forward).
+  int span_lo = 0, span_hi = NK;
+  if constexpr (MASK) {
+    if (a.mranges != nullptr) {
+      const int32_t* rr =
+          a.mranges + 2 * (b * a.mrsb + hq * a.mrsh + (int64_t)min(qrow, N - 1) * a.mrsq);
+      span_lo = rr[0];
+      span_hi = rr[1];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        span_lo = min(span_lo, __shfl_xor(span_lo, d));
+        span_hi = max(span_hi, __shfl_xor(span_hi, d));
+      }
+      int* const xs = (int*)k_lds1;
+      if (lane == 0) {
+        xs[2 * wave] = span_lo;
+        xs[2 * wave + 1] = span_hi;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        span_lo = min(span_lo, xs[2 * w2]);
+        span_hi = max(span_hi, xs[2 * w2 + 1]);
+      }
+      __syncthreads();  // every wave has read the exchange before a tile lands there
+      span_lo = __builtin_amdgcn_readfirstlane(span_lo);
+      span_hi = __builtin_amdgcn_readfirstlane(span_hi);
+    }
+  }
+  const int kv_len = min(CAUSAL ? max(0, min(NK, q0 + kBwdBlockRows + a.diag)) : NK, span_hi);
   const int ntiles = (kv_len + kBlockN - 1) / kBlockN;
+  const int j_begin = span_lo < span_hi ? min(span_lo / kBlockN, ntiles) : ntiles;
   // MASK: the lane's mask row (rows past N read row N - 1; not stored).
   const uint64_t* mrow =
       MASK ? a.mbits + b * a.msb + hq * a.msh + (int64_t)min(qrow, N - 1) * a.msq : nullptr;
@@ -719,9 +796,11 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
   }
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
-  if (ntiles > 0) issue(0, k_lds0, v_lds0);
+  // Tile j sits in the buffers of parity j & 1.
+  if (ntiles > j_begin)
+    issue(j_begin, (j_begin & 1) ? k_lds1 : k_lds0, (j_begin & 1) ? v_lds1 : v_lds0);
   barrier_after_loads<0>();
-  int j = 0;
+  int j = j_begin;
   for (; j + 1 < j_split; j += 2) {
     step(j, P0{}, Flag<false>{});
     step(j + 1, P1{}, Flag<false>{});

@@ -321,6 +321,15 @@ int validate_bwd(const fa_bwd_params* p) {
     if ((p->seq_len * p->mask_stride_q + words) * 8 > (int64_t)INT32_MAX)
       return fail(FA_ERR_TOO_LARGE, "seq_len * mask row stride exceeds 2^31 bytes");
   }
+  if (p->mask_ranges != nullptr) {
+    if (p->mask_bits == nullptr)
+      return fail(FA_ERR_INVALID_ARGUMENT, "mask_ranges needs mask_bits");
+    if ((reinterpret_cast<uintptr_t>(p->mask_ranges) & 7u) != 0)
+      return fail(FA_ERR_MISALIGNED, "mask_ranges must be 8-byte aligned");
+    if (p->mask_ranges_stride_b < 0 || p->mask_ranges_stride_h < 0 ||
+        p->mask_ranges_stride_q < 0)
+      return fail(FA_ERR_INVALID_ARGUMENT, "mask_ranges strides must be non-negative");
+  }
   const int64_t need = fa::bwd_workspace_bytes(p->batch, p->heads_q, p->seq_len);
   if (p->workspace_bytes < need)
     return fail(FA_ERR_INVALID_ARGUMENT, "workspace_bytes %lld is below the required %lld",
@@ -556,6 +565,10 @@ int fa_sm75_backward(const fa_bwd_params* p) {
   a.msb = p->mask_stride_b;
   a.msh = p->mask_stride_h;
   a.msq = p->mask_stride_q;
+  a.mranges = p->mask_ranges;
+  a.mrsb = p->mask_ranges_stride_b;
+  a.mrsh = p->mask_ranges_stride_h;
+  a.mrsq = p->mask_ranges_stride_q;
   a.n = (int)p->seq_len;
   a.nk = (int)bwd_kv_rows(p);
   a.diag = p->causal == FA_CAUSAL_BOTTOM_RIGHT ? a.nk - a.n : 0;

@@ -158,6 +158,8 @@ struct BwdArgs {
   float* stats;
   const uint64_t* mbits;   // explicit mask bits (fa_fwd_params layout) or nullptr
   int64_t msb, msh, msq;   // its strides in 64-bit words
+  const int32_t* mranges;  // per mask row (first, one past last) visible key, or nullptr
+  int64_t mrsb, mrsh, mrsq;  // its strides in pairs
   int mwords;              // ceil(nk / 64): words of one mask row
   int n;       // query rows
   int nk;      // key/value rows

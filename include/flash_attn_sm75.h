@@ -275,6 +275,12 @@ typedef struct fa_bwd_params {
    * (AND) with `causal`.  The LSE must come from a forward with this mask. */
   const uint64_t* mask_bits;
   int64_t mask_stride_b, mask_stride_h, mask_stride_q;
+  /* Optional, with mask_bits: each mask row's span of visible keys, as in
+   * fa_fwd_params.mask_ranges.  The dQ kernel then skips the key tiles no
+   * row of its block sees, the dK/dV kernel the query tiles with no row that
+   * sees a key of its block. */
+  const int32_t* mask_ranges;
+  int64_t mask_ranges_stride_b, mask_ranges_stride_h, mask_ranges_stride_q;
 } fa_bwd_params;
 
 /* Fills contiguous strides for every tensor of *p from its sizes. */

@@ -52,4 +52,6 @@ class BwdParams(ctypes.Structure):
         ("workspace_bytes", ctypes.c_int64),
         ("mask_bits", ctypes.c_void_p), ("mask_stride_b", ctypes.c_int64),
         ("mask_stride_h", ctypes.c_int64), ("mask_stride_q", ctypes.c_int64),
+        ("mask_ranges", ctypes.c_void_p), ("mask_ranges_stride_b", ctypes.c_int64),
+        ("mask_ranges_stride_h", ctypes.c_int64), ("mask_ranges_stride_q", ctypes.c_int64),
     ]

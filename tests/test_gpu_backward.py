@@ -361,3 +361,71 @@ def test_side_stream(device):
     torch.cuda.synchronize()
     for x, y in zip(want, got):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,bf16", [(3, 4, 2, 700, 64, False), (2, 8, 2, 1100, 128, True)])
+def test_backward_mask_ranges_bitwise(device, B, Hq, Hkv, N, D, bf16):
+    """Through the C ABI: a causal mask with left padding given as bits, with
+    and without mask_ranges: dQ, dK and dV bit for bit the same (the skipped
+    key tiles of dQ and query tiles of dK/dV see nothing of each other), and
+    within the bar of the float64 closed form."""
+    import ctypes
+    from capi_types import LIB, BwdParams
+    print(f"[bwd ranges] B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} bf16={bf16}", flush=True)
+    lib = ctypes.CDLL(LIB)
+    lib.fa_sm75_backward.argtypes = [ctypes.POINTER(BwdParams)]
+    lib.fa_sm75_backward_workspace_size.argtypes = [ctypes.POINTER(BwdParams)]
+    lib.fa_sm75_backward_workspace_size.restype = ctypes.c_int64
+    lib.fa_sm75_set_contiguous_bwd_strides.argtypes = [ctypes.POINTER(BwdParams)]
+    lib.fa_sm75_last_error.restype = ctypes.c_char_p
+    pk = lib.fa_sm75_pack_mask_ranges
+    pk.argtypes = [ctypes.c_void_p] + [ctypes.c_int64] * 8 + [ctypes.c_void_p] * 3
+    dt = torch.bfloat16 if bf16 else torch.float16
+    g = torch.Generator("cpu").manual_seed(N + D)
+    q, k, v, do = (torch.randn(B, h, N, D, generator=g).to(dt) for h in (Hq, Hkv, Hkv, Hq))
+    i = torch.arange(N)
+    m = (i[None, :] <= i[:, None])[None, None].expand(B, 1, N, N).clone()
+    for b in range(B):
+        m[b, :, :, : (b * N) // (2 * B)] = False
+    qd, kd, vd, dod, md = (t.to(device) for t in (q, k, v, do, m))
+    o, lse = flash_attention_forward_ex(qd, kd, vd, attn_mask=md, return_lse=True)
+    words = (N + 63) // 64
+    bits = torch.empty(B, 1, N, words, dtype=torch.int64, device=device)
+    rng = torch.empty(B, 1, N, 2, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    st = md.stride()
+    assert pk(md.data_ptr(), B, 1, N, N, st[0], 0, st[2], st[3], bits.data_ptr(), rng.data_ptr(),
+              stream) == 0
+
+    def run(with_ranges):
+        dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+        p = BwdParams()
+        p.q, p.k, p.v, p.o, p.dout, p.lse, p.dq, p.dk, p.dv = (
+            t.data_ptr() for t in (qd, kd, vd, o, dod, lse, dq, dk, dv))
+        p.batch, p.heads_q, p.heads_kv, p.seq_len, p.seq_len_kv, p.head_dim = B, Hq, Hkv, N, N, D
+        lib.fa_sm75_set_contiguous_bwd_strides(ctypes.byref(p))
+        p.scale, p.dtype, p.stream = D ** -0.5, 1 if bf16 else 0, stream
+        p.mask_bits, p.mask_stride_b, p.mask_stride_q = bits.data_ptr(), N * words, words
+        if with_ranges:
+            p.mask_ranges, p.mask_ranges_stride_b, p.mask_ranges_stride_q = rng.data_ptr(), N, 1
+        n = lib.fa_sm75_backward_workspace_size(ctypes.byref(p))
+        ws = torch.empty(n, dtype=torch.uint8, device=device)
+        p.workspace, p.workspace_bytes = ws.data_ptr(), n
+        assert lib.fa_sm75_backward(ctypes.byref(p)) == 0, lib.fa_sm75_last_error()
+        torch.cuda.synchronize()
+        return dq, dk, dv
+
+    with_r = run(True)
+    without = run(False)
+    for a_, b_ in zip(with_r, without):
+        assert torch.equal(a_, b_)
+    npf = lambda t: t.float().cpu().numpy()
+    wants = ref.attention_backward_f64(npf(q), npf(k), npf(v), npf(do), attn_mask=m.numpy(),
+                                       delta_from_o=npf(o))
+    ba, br = (1e-2, 4e-2) if bf16 else (2e-3, 1e-2)
+    for name, gt, w in zip(("dQ", "dK", "dV"), with_r, wants):
+        gg = npf(gt).astype(np.float64)
+        sc = max(float(np.abs(w).max()), 1e-2)
+        worst = float((np.abs(gg - w) / (ba * sc + br * np.abs(w) + 1e-30)).max())
+        print(f"  {name}: worst/bar={worst:.3f}", flush=True)
+        assert worst <= 1.0, (name, worst)
