@@ -39,7 +39,7 @@ those calls over its wall time.  Besides the driver's keys the line holds
                 against a KV cache): median call time and HBM rate;
   widened       the calls beyond the reference's fp16 square launches on the
                 C4 shape: bfloat16 forward and backward, a key-padding boolean
-                mask, and a chunked prefill (Nq=2048 against Nk=8192,
+                mask, the causal mask as a bool tensor, and a chunked prefill (Nq=2048 against Nk=8192,
                 bottom-right causal): average call time and TFLOPS; and a
                 padded-batch decode (D1 with a key-padding mask): GB/s.
 Diagnostics go to stderr.
@@ -435,9 +435,10 @@ def time_calls(fn, steps=20, warm_ms=100.0):
 def time_widened(steps=20):
     """The calls the hot path was widened to, beyond the reference's fp16
     square launches: bfloat16 forward and backward on the C4 shape, C4 with a
-    key-padding boolean mask (the masked kernel), a padded-batch decode (D1
-    with a key-padding mask) and a chunked prefill (2048 new rows against
-    8192 cached keys, bottom-right causal)."""
+    key-padding boolean mask (the masked kernel), C4 with its causal mask as a
+    bool tensor (transformers' form), a padded-batch decode (D1 with a
+    key-padding mask) and a chunked prefill (2048 new rows against 8192
+    cached keys, bottom-right causal)."""
     import torch
 
     from flash_attention_sm75 import flash_attention_forward_ex
@@ -467,6 +468,19 @@ def time_widened(steps=20):
     out["mask_fwd"] = {"workload": "C4 shape, causal and a [B,1,1,N] key-padding mask "
                                    "(last 10% hidden); FLOPs counted as unmasked causal",
                        "ms": round(ms, 5), "tflops": round(F / (ms * 1e-3) / 1e12, 1)}
+
+    # The causal mask as transformers hands it over for a padded prefill: a
+    # materialised bool [B, 1, N, N] tensor with is_causal false (packed to
+    # bits with each row's span of visible keys, so the kernel skips the
+    # upper triangle); FLOPs counted as causal, the packing inside the call.
+    i_ = torch.arange(N, device=dev)
+    tri = (i_[None, :] <= i_[:, None])[None, None].expand(B, 1, N, N).contiguous()
+    ms = time_calls(lambda: flash_attention_forward_ex(q, k, v, attn_mask=tri), steps)
+    out["bool_causal_fwd"] = {"workload": "C4 shape, the causal mask as a bool [B,1,N,N] tensor "
+                                          "with is_causal false (transformers' form); FLOPs "
+                                          "counted as causal",
+                              "ms": round(ms, 5), "tflops": round(F / (ms * 1e-3) / 1e12, 1)}
+    del tri
 
     # Padded-batch decode: D1's shape (a batched Llama-style decode step), the
     # sequences of the batch of lengths Nk/2 .. Nk (a [B,1,1,Nk] key-padding
