@@ -12,10 +12,13 @@
 // dK/dV kernel forms dS from the rounded P its dV product takes, the dQ
 // kernel from the unrounded P (both within one rounding of each other).
 //
-// Three kernels, all deterministic (no atomics: every gradient element is
-// summed by one wave in a fixed order):
-//   * fa_bwd_stats_kernel: per query row lse * log2(e) and -rowsum(dO o O),
-//     into the workspace in 64-row records (one direct load per tile).
+// Two kernels, all deterministic (no atomics: every gradient element is
+// summed by one wave in a fixed order), dQ launched first:
+//   * fa_bwd_dq_kernel: one workgroup per (batch, query head, 128 rows), the
+//     forward's shape: Q and dO rows resident, K and V tiles streamed through
+//     double-buffered LDS; two workgroups per CU.  It also forms each row's
+//     lse * log2(e) and -rowsum(dO o O) and writes them to the workspace in
+//     64-row records (one direct load per tile for the next kernel).
 //   * fa_bwd_dkdv_kernel: one workgroup of 8 waves per (batch, KV head, 128
 //     keys); waves w and w+4 own keys k0 + 32w .. +32 and split the four
 //     products (w: S, P, dV with the K rows resident; w+4: dP, dS, dK with
@@ -24,9 +27,6 @@
 //     buffered LDS for every query head of the group, so the GQA sum over
 //     the group happens in the accumulators; one workgroup per CU, two waves
 //     per SIMD.
-//   * fa_bwd_dq_kernel: one workgroup per (batch, query head, 128 rows), the
-//     forward's shape: Q and dO rows resident, K and V tiles streamed through
-//     double-buffered LDS; two workgroups per CU.
 // An explicit boolean mask (MASK instances) hides keys on top of the causal
 // rule; rows that see no key have lse = -inf, so their P is 0.
 // Tiles use the forward's LDS layout (Lds<D>: padded rows, 16-byte chunks
@@ -106,50 +106,6 @@ __device__ __forceinline__ int seg_offset(int seg, int lane, int64_t stride) {
 template <class E, int NOPS>
 __device__ __forceinline__ void put_pair(uint4v (&ops)[NOPS], int t, int i, float x, float y) {
   ops[2 * t + (i >> 3)][(i & 7) >> 1] = __builtin_bit_cast(unsigned, E::pack(x, y));
-}
-
-// ---- stats: lse * log2(e) and -rowsum(dO o O) per query row ----------------
-// One workgroup per (b, query head, 64-row tile); wave w takes rows 16w..16w+15,
-// D/8 lanes per row (16 bytes each).
-template <int D, bool BF16>
-__global__ void __launch_bounds__(256) fa_bwd_stats_kernel(const BwdArgs a) {
-  using E = Elem<BF16>;
-  constexpr int LPR = D / 8;      // lanes per row
-  constexpr int RPP = 64 / LPR;   // rows per pass
-  const int rec = (int)blockIdx.x;  // (b * hq + h) * qtiles + qt
-  const int bh = rec / a.qtiles;
-  const int qt = rec - bh * a.qtiles;
-  const int b = bh / a.hq, hq = bh - b * a.hq;
-  const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
-  const int sub = lane / LPR, part = lane - sub * LPR;
-  float* const out = a.stats + (int64_t)rec * (2 * kBwdStatsTile);
-#pragma unroll
-  for (int r0 = 16 * wave; r0 < 16 * wave + 16; r0 += RPP) {
-    const int r = r0 + sub;
-    const int row = qt * kBwdStatsTile + r;
-    float acc = 0.0f;
-    if (row < a.n) {
-      // Non-temporal loads: O is read once here (dO again by the other kernels,
-      // long after).
-      const half8 o8 = __builtin_nontemporal_load(
-          (const half8*)(a.o + b * a.osb + hq * a.osh + (int64_t)row * a.osn + 8 * part));
-      const half8 d8 = __builtin_nontemporal_load(
-          (const half8*)(a.dout + b * a.dosb + hq * a.dosh + (int64_t)row * a.dosn + 8 * part));
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(E::to_f32(o8[j]), E::to_f32(d8[j]), acc);
-    }
-#pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-    if (part == 0) {
-      float l2 = __builtin_inff();
-      if (row < a.n) {
-        const float l = a.lse[(int64_t)bh * a.n + row];
-        l2 = (l == -__builtin_inff()) ? __builtin_inff() : l * 1.4426950408889634f;
-      }
-      out[r] = l2;
-      out[kBwdStatsTile + r] = row < a.n ? -acc : 0.0f;
-    }
-  }
 }
 
 typedef float float4v __attribute__((ext_vector_type(4)));
@@ -653,23 +609,44 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
   const int qrow = qw + ql;
   const int N = a.n, NK = a.nk;
 
-  // Q and dO rows of the lane's query as B operands (n = query, k = dims).
+  // Q and dO rows of the lane's query as B operands (n = query, k = dims),
+  // and the row's statistics: lse2 = lse * log2(e) (+inf for a row that sees
+  // no key) and ndelta = -rowsum(dO o O), each half-wave summing the dims
+  // it holds (O is read once, here).
   half8 qf[KK], df[KK];
-  float lse2 = __builtin_inff(), ndelta = 0.0f;
+  float lse2 = __builtin_inff(), dot = 0.0f;
   if (qrow < N) {
     const _Float16* qp = a.q + b * a.qsb + hq * a.qsh + (int64_t)qrow * a.qsn + 8 * hi;
     const _Float16* dp = a.dout + b * a.dosb + hq * a.dosh + (int64_t)qrow * a.dosn + 8 * hi;
+    const _Float16* op = a.o + b * a.osb + hq * a.osh + (int64_t)qrow * a.osn + 8 * hi;
+    half8 of[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       qf[kk] = *(const half8*)(qp + 16 * kk);
       df[kk] = *(const half8*)(dp + 16 * kk);
+      of[kk] = __builtin_nontemporal_load((const half8*)(op + 16 * kk));
     }
-    const float* st = a.stats + ((int64_t)bh * a.qtiles + qrow / kBwdStatsTile) * (2 * kBwdStatsTile);
-    lse2 = st[qrow % kBwdStatsTile];
-    ndelta = st[kBwdStatsTile + qrow % kBwdStatsTile];
+    const float l = a.lse[(int64_t)bh * N + qrow];
+    lse2 = (l == -__builtin_inff()) ? __builtin_inff() : l * 1.4426950408889634f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        dot = __builtin_fmaf(E::to_f32(of[kk][e]), E::to_f32(df[kk][e]), dot);
+    }
   } else {
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) qf[kk] = df[kk] = (half8)(_Float16)0;
+  }
+  dot += __shfl_xor(dot, 32);
+  const float ndelta = qrow < N ? -dot : 0.0f;
+  // The dK/dV kernel, launched after this one, reads them from the workspace:
+  // one record per (b, query head, 64-row tile), rows past N as (+inf, 0).
+  if (hi == 0 && qrow / kBwdStatsTile < a.qtiles) {
+    float* const st =
+        a.stats + ((int64_t)bh * a.qtiles + qrow / kBwdStatsTile) * (2 * kBwdStatsTile);
+    st[qrow % kBwdStatsTile] = lse2;
+    st[kBwdStatsTile + qrow % kBwdStatsTile] = ndelta;
   }
   float16v dq[MT];
 #pragma unroll
@@ -828,29 +805,28 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
 
 }  // namespace
 
-// Launches the three backward kernels for head dimension D (the launcher in
+// Launches the two backward kernels for head dimension D (the launcher in
 // fa_bwd.hip has planned the grids).
 template <int D, bool BF16, bool MASK>
 void launch_bwd(const BwdArgs& a, int batch, bool causal, hipStream_t stream) {
-  const int stats_wgs = batch * a.hq * a.qtiles;
   const int dkdv_wgs = a.units * ((a.nk + kBwdBlockKeys - 1) / kBwdBlockKeys);
   const int dq_wgs = a.items;
-  if (stats_wgs > 0)
-    hipLaunchKernelGGL((fa_bwd_stats_kernel<D, BF16>), dim3(stats_wgs), dim3(256), 0, stream, a);
+  // dQ first: it writes the row statistics the dK/dV kernel reads (its grid
+  // covers every query row, a.items = batch * heads * ceil(n / 128)).
   if (causal) {
-    if (dkdv_wgs > 0)
-      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, true, MASK, BF16>), dim3(dkdv_wgs), dim3(512), 0,
-                         stream, a);
     if (dq_wgs > 0)
       hipLaunchKernelGGL((fa_bwd_dq_kernel<D, true, MASK, BF16>), dim3(dq_wgs), dim3(256), 0, stream,
                          a);
-  } else {
     if (dkdv_wgs > 0)
-      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, false, MASK, BF16>), dim3(dkdv_wgs), dim3(512), 0,
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, true, MASK, BF16>), dim3(dkdv_wgs), dim3(512), 0,
                          stream, a);
+  } else {
     if (dq_wgs > 0)
       hipLaunchKernelGGL((fa_bwd_dq_kernel<D, false, MASK, BF16>), dim3(dq_wgs), dim3(256), 0, stream,
                          a);
+    if (dkdv_wgs > 0)
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, false, MASK, BF16>), dim3(dkdv_wgs), dim3(512), 0,
+                         stream, a);
   }
 }
 

@@ -132,7 +132,7 @@ int launch_decode_forward(const FwdArgs& a, const DecodePlan& plan, int head_dim
                           void* workspace, hipStream_t stream);
 
 // ---- Backward (fa_bwd.hip, fa_bwd_kernel.h) --------------------------------
-// Kernel arguments of the three backward kernels (passed by value).  The
+// Kernel arguments of the two backward kernels (passed by value).  The
 // grid-plan fields carry the names block_work reads.
 struct BwdArgs {
   const _Float16* q;
@@ -154,7 +154,7 @@ struct BwdArgs {
   int64_t dvsb, dvsh, dvsn;
   // Workspace: per (b, query head) and 64-row query tile, 64 floats
   // lse * log2(e) (+inf for rows past N and rows that see no key), then 64
-  // floats rowsum(dO * O) (0 past N).
+  // floats -rowsum(dO * O) (0 past N); the dQ kernel writes it.
   float* stats;
   const uint64_t* mbits;   // explicit mask bits (fa_fwd_params layout) or nullptr
   int64_t msb, msh, msq;   // its strides in 64-bit words
@@ -184,7 +184,7 @@ inline int64_t bwd_workspace_bytes(int64_t batch, int64_t heads_q, int64_t seq_l
   return batch * heads_q * ((seq_len + kBwdStatsTile - 1) / kBwdStatsTile) *
          (2 * kBwdStatsTile) * (int64_t)sizeof(float);
 }
-// Launches the stats, dK/dV and dQ kernels; all arguments validated.
+// Launches the dQ and dK/dV kernels; all arguments validated.
 int launch_backward(const BwdArgs& a, int batch, int head_dim, bool causal, bool bf16,
                     hipStream_t stream);
 template <int D, bool BF16, bool MASK>

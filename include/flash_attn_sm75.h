@@ -286,8 +286,8 @@ typedef struct fa_bwd_params {
 /* Fills contiguous strides for every tensor of *p from its sizes. */
 void fa_sm75_set_contiguous_bwd_strides(fa_bwd_params* p);
 
-/* Backward: three kernels on p->stream (per-row statistics into the
- * workspace, then dK/dV, then dQ).  Asynchronous; validates every argument
+/* Backward: two kernels on p->stream (dQ, which also writes per-row
+ * statistics into the workspace, then dK/dV).  Asynchronous; validates every argument
  * before touching the device.  Returns FA_OK or an fa_status. */
 int fa_sm75_backward(const fa_bwd_params* p);
 
