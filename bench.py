@@ -375,9 +375,9 @@ def time_sdpa_decode_call(keys, n=200):
 
 
 def time_backward(cfg, steps=10, warmup=3, dtype="fp16", warm_ms=200.0):
-    """Average time of one flash_attention_backward call (stats, dK/dV and dQ
-    kernels) on the workload's shape, HIP events on the launch stream around
-    the timed calls, after W warm-up calls and at least warm_ms of them (the
+    """Average time of one flash_attention_backward call (the dQ kernel, which
+    also forms the row statistics, then dK/dV) on the workload's shape, HIP
+    events on the launch stream around the timed calls, after W warm-up calls and at least warm_ms of them (the
     clock settles after a change of load); inputs, O, LSE and dO resident in
     HBM."""
     import torch
@@ -729,7 +729,7 @@ def main():
             "flop": int(2.5 * F),
             "flop_convention": "2.5x the forward's (5 matrix products: QK^T, dP, dV, dK, dQ); "
                                "the kernels execute 3.5x (dQ recomputes QK^T and dP)",
-            "kernels": "fa_bwd_stats + fa_bwd_dkdv + fa_bwd_dq, deterministic, fp16",
+            "kernels": "fa_bwd_dq (+ row statistics) then fa_bwd_dkdv, deterministic, fp16",
         }
         log(f"[{cfg} backward] {backward}")
 
