@@ -3,6 +3,7 @@
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C4]
                   [--no-cpu-baseline] [--no-gemm-ceiling] [--all] [--decode] [--hf]
                   [--shape B,Hq,Hkv,N,D,causal] [--no-backward] [--no-configs] [--no-widened]
+                  [--no-sweep]
 
 A step is one fused forward over one batch of synthetic input (the hot path:
 flash_attention_sm75.flash_attention_forward -> flash_attn_sm75_cuda ->
@@ -41,7 +42,12 @@ those calls over its wall time.  Besides the driver's keys the line holds
                 C4 shape: bfloat16 forward and backward, a key-padding boolean
                 mask, the causal mask as a bool tensor, and a chunked prefill (Nq=2048 against Nk=8192,
                 bottom-right causal): average call time and TFLOPS; and a
-                padded-batch decode (D1 with a key-padding mask): GB/s.
+                padded-batch decode (D1 with a key-padding mask): GB/s;
+  sweep         the reference's head_dim sweep (benchmarks/benchmark_d64_d128.py:
+                91-98: B=1 H=8 N=128..4096, B=1 H=32 and B=4 H=8 at N=512 and
+                1024, head_dim 64 and 128, full and causal): back-to-back
+                launch average, TFLOPS, fraction of peak, and torch's SDPA on
+                the same inputs.
 Diagnostics go to stderr.
 """
 import argparse
@@ -518,6 +524,44 @@ def time_widened(steps=20):
     return out
 
 
+# The reference's head_dim sweep (benchmarks/benchmark_d64_d128.py:91-98):
+# (B, H, N, D, causal), H query heads = KV heads, N(0,1) fp16 inputs.
+SWEEP = ([(1, 8, n, d, c) for c in (False, True) for d in (64, 128)
+          for n in (128, 256, 512, 1024, 2048, 4096)]
+         + [s for c in (False, True) for d in (64, 128) for n in (512, 1024)
+            for s in ((1, 32, n, d, c), (4, 8, n, d, c))])
+
+
+def time_sweep(steps=20, warm_ms=30.0):
+    """Every shape of the reference's head_dim sweep: the fused forward's
+    average over `steps` launches issued back to back (one HIP event pair on
+    the launch stream, after at least warm_ms of launches), its TFLOPS and
+    fraction of the MFMA peak, and torch's own SDPA on the same inputs timed
+    the same way (the reference's sweep reports its kernel against SDPA,
+    benchmarks/benchmark_d64_d128.py:60-88)."""
+    import torch
+    import torch.nn.functional as tF
+
+    from flash_attention_sm75 import flash_attention_forward
+
+    dev = torch.device("cuda", 0)
+    out = []
+    for i, (B, H, N, D, causal) in enumerate(SWEEP):
+        g = torch.Generator("cpu").manual_seed(100 + i)
+        q, k, v = (torch.randn(B, H, N, D, generator=g).half().to(dev) for _ in range(3))
+        F_ = flops(B, H, N, D, causal)
+        ms = time_calls(lambda: flash_attention_forward(q, k, v, causal=causal), steps, warm_ms)
+        sdpa_ms = time_calls(lambda: tF.scaled_dot_product_attention(q, k, v, is_causal=causal),
+                             steps, warm_ms)
+        tf = F_ / (ms * 1e-3) / 1e12
+        out.append({"B": B, "H": H, "N": N, "D": D, "causal": causal,
+                    "kernel_avg_ms": round(ms, 5), "tflops": round(tf, 1),
+                    "frac": round(tf / PEAK_TFLOPS, 4), "sdpa_ms": round(sdpa_ms, 5),
+                    "vs_sdpa": round(sdpa_ms / ms, 3)})
+        del q, k, v
+    return out
+
+
 def time_hf(prompt_len=4096, decode_steps=32):
     """Random-init Qwen2-0.5B-shaped model (no weights can be downloaded):
     prefill and teacher-forced KV-cache decode, unpatched vs patched SDPA."""
@@ -599,6 +643,8 @@ def main():
                     help="skip timing the other BASELINE configurations (C1-C5)")
     ap.add_argument("--no-backward", action="store_true",
                     help="skip timing the backward pass on the same workload")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the reference's head_dim sweep (d64/d128 x N x full/causal)")
     ap.add_argument("--no-widened", action="store_true",
                     help="skip timing the widened calls (bf16, boolean mask, chunked prefill)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -753,6 +799,15 @@ def main():
         widened = time_widened(args.steps)
         log(f"[widened] {widened}")
 
+    sweep = None
+    if not args.no_sweep and args.data == "randn" and cfg in CONFIGS:
+        sweep = time_sweep(args.steps)
+        for r in sweep:
+            log(f"[sweep] B={r['B']} H={r['H']} N={r['N']} d={r['D']} "
+                f"{'causal' if r['causal'] else 'full'}: {r['kernel_avg_ms']:.4f} ms -> "
+                f"{r['tflops']:.1f} TFLOPS ({100 * r['frac']:.1f}%); sdpa {r['sdpa_ms']:.4f} ms "
+                f"({r['vs_sdpa']:.2f}x)")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.cpu_budget)
@@ -795,6 +850,7 @@ def main():
         "backward": backward,
         "decode": decode,
         "widened": widened,
+        "sweep": sweep,
     }
     print(json.dumps(line), flush=True)
 

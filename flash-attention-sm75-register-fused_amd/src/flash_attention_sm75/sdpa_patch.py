@@ -13,10 +13,11 @@ without changing results:
     kernel instead of falling back; ``is_causal`` keeps SDPA's top-left
     alignment (key j visible to query i iff j <= i);
   * boolean ``attn_mask`` (what transformers builds for padded batches) runs
-    on the kernel too, also together with ``is_causal`` (the key must pass
-    both, which is what torch's CPU SDPA computes for the pair; torch's GPU
-    path on ROCm returns results that differ from call to call for it);
-    additive float masks fall back;
+    on the kernel too; additive float masks fall back, and so does a mask
+    given together with ``is_causal`` (reason ``mask_and_causal``): torch
+    documents that pair as an error, and its behaviour differs between
+    devices and builds, so the call goes to torch unchanged and raises (or
+    returns) exactly what the unpatched call does;
   * Q/K/V views are read in place (transformers passes [B, N, H, D] buffers
     viewed as [B, H, N, D]) and O keeps Q's layout, so the caller's
     ``transpose(1, 2).contiguous()`` is free;
@@ -66,6 +67,8 @@ def _fallback_reason(query, key, value, attn_mask, dropout_p, is_causal, kwargs)
         return "dropout"
     if attn_mask is not None and attn_mask.dtype != torch.bool:
         return "has_attn_mask"  # additive float masks stay with torch
+    if attn_mask is not None and is_causal:
+        return "mask_and_causal"  # torch's own call decides (it documents an error)
     if key.size(0) != query.size(0):
         return "batch_mismatch"
     if key.size(1) == 0 or query.size(1) % key.size(1) != 0:

@@ -320,7 +320,15 @@ def flops(batch, heads, seq_len, head_dim, causal=False):
 # CPU baseline (same ops as attention_ref.py:28-45, evaluated per (b, h) and
 # row block so the [N, N] score matrix fits in host memory).
 # ---------------------------------------------------------------------------
-def attention_reference_torch_cpu(Q, K, V, causal=False, scale=None, rows=2048, heads=None):
+def attention_reference_torch_cpu(Q, K, V, causal=False, scale=None, rows=2048, heads=None,
+                                  return_f32=False, skip_hidden=False):
+    """Square (Nq == Nk) attention per (b, h) and row block with torch on the
+    CPU.  Defaults: the reference's op order, full [rows, N] score blocks
+    masked afterwards, fp16 output (the timed CPU baseline).  return_f32
+    keeps the unrounded fp32 result (parity checks hold the kernel to the
+    unrounded value); skip_hidden evaluates a causal row block only up to its
+    last row's diagonal (the keys past it are hidden from every row of the
+    block and add exp(-inf) = 0), which halves the work of a causal check."""
     import torch
 
     B, Hq, N, D = Q.shape
@@ -329,18 +337,20 @@ def attention_reference_torch_cpu(Q, K, V, causal=False, scale=None, rows=2048, 
     if scale is None:
         scale = default_scale(D)
     hs = list(range(Hq)) if heads is None else list(heads)
-    out = torch.empty((B, len(hs), N, D), dtype=torch.float16)
+    out = torch.empty((B, len(hs), N, D), dtype=torch.float32 if return_f32 else torch.float16)
     for b in range(B):
         for oi, h in enumerate(hs):
             k_f = K[b, h // group].float()
             v_f = V[b, h // group].float()
             for r0 in range(0, N, rows):
                 r1 = min(N, r0 + rows)
+                kc = r1 if causal and skip_hidden else N
                 q_f = Q[b, h, r0:r1].float()
-                S = torch.matmul(q_f, k_f.transpose(-2, -1)) * scale
+                S = torch.matmul(q_f, k_f[:kc].transpose(-2, -1)) * scale
                 if causal:
-                    mask = torch.ones(r1 - r0, N, dtype=torch.bool).triu(diagonal=1 + r0)
+                    mask = torch.ones(r1 - r0, kc, dtype=torch.bool).triu(diagonal=1 + r0)
                     S.masked_fill_(mask, float("-inf"))
                 P = torch.softmax(S, dim=-1)
-                out[b, oi, r0:r1] = torch.matmul(P, v_f).half()
+                o = torch.matmul(P, v_f[:kc])
+                out[b, oi, r0:r1] = o if return_f32 else o.half()
     return out

@@ -363,15 +363,42 @@ def test_side_stream(device):
         assert torch.equal(x, y)
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,N,D,bf16", [(3, 4, 2, 700, 64, False), (2, 8, 2, 1100, 128, True)])
-def test_backward_mask_ranges_bitwise(device, B, Hq, Hkv, N, D, bf16):
-    """Through the C ABI: a causal mask with left padding given as bits, with
-    and without mask_ranges: dQ, dK and dV bit for bit the same (the skipped
-    key tiles of dQ and query tiles of dK/dV see nothing of each other), and
-    within the bar of the float64 closed form."""
+def per_head_mask(B, Hq, N, seed):
+    """[B, Hq, N, N] boolean mask that differs between the query heads of a
+    KV group: head h sees a causal sliding window of its own width (one head
+    the whole causal prefix), a tenth of the window's keys dropped at
+    random, and a block of rows of every odd head sees no key at all.  The
+    dK/dV kernel then has to take the union of the rows' key spans over the
+    group's heads to find the query tiles of its key block."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    i = torch.arange(N)
+    m = torch.zeros(B, Hq, N, N, dtype=torch.bool)
+    for h in range(Hq):
+        w = [N, 37, 150, 400][h % 4] + 13 * (h // 4)
+        band = (i[None, :] <= i[:, None]) & (i[None, :] > i[:, None] - w)
+        for b in range(B):
+            keep = torch.rand(N, N, generator=g) >= 0.1
+            m[b, h] = band & keep
+            if h % 2 == 1:
+                r0 = (97 * (h + b)) % (N - 80)
+                m[b, h, r0:r0 + 70] = False
+    return m
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,bf16,per_head",
+                         [(3, 4, 2, 700, 64, False, False), (2, 8, 2, 1100, 128, True, False),
+                          (2, 8, 2, 600, 64, False, True), (1, 6, 2, 900, 128, False, True)])
+def test_backward_mask_ranges_bitwise(device, B, Hq, Hkv, N, D, bf16, per_head):
+    """Through the C ABI: a mask given as bits, with and without mask_ranges:
+    dQ, dK and dV bit for bit the same (the skipped key tiles of dQ and query
+    tiles of dK/dV see nothing of each other), and within the bar of the
+    float64 closed form.  The mask is a causal one with left padding shared
+    by every head, or (per_head) a [B, Hq, N, N] mask whose rows' spans differ
+    between the query heads of a group and some of whose rows see no key."""
     import ctypes
     from capi_types import LIB, BwdParams
-    print(f"[bwd ranges] B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} bf16={bf16}", flush=True)
+    print(f"[bwd ranges] B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} bf16={bf16} per_head={per_head}",
+          flush=True)
     lib = ctypes.CDLL(LIB)
     lib.fa_sm75_backward.argtypes = [ctypes.POINTER(BwdParams)]
     lib.fa_sm75_backward_workspace_size.argtypes = [ctypes.POINTER(BwdParams)]
@@ -383,19 +410,25 @@ def test_backward_mask_ranges_bitwise(device, B, Hq, Hkv, N, D, bf16):
     dt = torch.bfloat16 if bf16 else torch.float16
     g = torch.Generator("cpu").manual_seed(N + D)
     q, k, v, do = (torch.randn(B, h, N, D, generator=g).to(dt) for h in (Hq, Hkv, Hkv, Hq))
-    i = torch.arange(N)
-    m = (i[None, :] <= i[:, None])[None, None].expand(B, 1, N, N).clone()
-    for b in range(B):
-        m[b, :, :, : (b * N) // (2 * B)] = False
+    if per_head:
+        m = per_head_mask(B, Hq, N, N + D)
+    else:
+        i = torch.arange(N)
+        m = (i[None, :] <= i[:, None])[None, None].expand(B, 1, N, N).clone()
+        for b in range(B):
+            m[b, :, :, : (b * N) // (2 * B)] = False
+    mh = m.size(1)
     qd, kd, vd, dod, md = (t.to(device) for t in (q, k, v, do, m))
     o, lse = flash_attention_forward_ex(qd, kd, vd, attn_mask=md, return_lse=True)
     words = (N + 63) // 64
-    bits = torch.empty(B, 1, N, words, dtype=torch.int64, device=device)
-    rng = torch.empty(B, 1, N, 2, dtype=torch.int32, device=device)
+    bits = torch.empty(B, mh, N, words, dtype=torch.int64, device=device)
+    rng = torch.empty(B, mh, N, 2, dtype=torch.int32, device=device)
     stream = torch.cuda.current_stream().cuda_stream
     st = md.stride()
-    assert pk(md.data_ptr(), B, 1, N, N, st[0], 0, st[2], st[3], bits.data_ptr(), rng.data_ptr(),
-              stream) == 0
+    assert pk(md.data_ptr(), B, mh, N, N, st[0], st[1] if mh > 1 else 0, st[2], st[3],
+              bits.data_ptr(), rng.data_ptr(), stream) == 0
+    if per_head:  # some rows see nothing: their range is empty
+        assert (rng[..., 0] >= rng[..., 1]).any().item()
 
     def run(with_ranges):
         dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
@@ -405,9 +438,11 @@ def test_backward_mask_ranges_bitwise(device, B, Hq, Hkv, N, D, bf16):
         p.batch, p.heads_q, p.heads_kv, p.seq_len, p.seq_len_kv, p.head_dim = B, Hq, Hkv, N, N, D
         lib.fa_sm75_set_contiguous_bwd_strides(ctypes.byref(p))
         p.scale, p.dtype, p.stream = D ** -0.5, 1 if bf16 else 0, stream
-        p.mask_bits, p.mask_stride_b, p.mask_stride_q = bits.data_ptr(), N * words, words
+        p.mask_bits, p.mask_stride_b, p.mask_stride_q = bits.data_ptr(), mh * N * words, words
+        p.mask_stride_h = N * words if mh > 1 else 0
         if with_ranges:
-            p.mask_ranges, p.mask_ranges_stride_b, p.mask_ranges_stride_q = rng.data_ptr(), N, 1
+            p.mask_ranges, p.mask_ranges_stride_b, p.mask_ranges_stride_q = rng.data_ptr(), mh * N, 1
+            p.mask_ranges_stride_h = N if mh > 1 else 0
         n = lib.fa_sm75_backward_workspace_size(ctypes.byref(p))
         ws = torch.empty(n, dtype=torch.uint8, device=device)
         p.workspace, p.workspace_bytes = ws.data_ptr(), n

@@ -146,30 +146,33 @@ def test_c3_causal(device):
     run_case(4, 8, 8, 2048, 64, True, seed=2)
 
 
-def one_head_per_unit(B, Hq, Hkv, shift=0):
-    """(batch, query head) pairs, one per (batch, KV head) unit, the query head
-    taken at a different position of each unit's group.  The kernels give each
-    unit its own XCD share (static order) or queue (dynamic schedule), so this
-    covers every XCD and every queue of a full-size launch."""
+def heads_per_unit(B, Hq, Hkv, per_unit=1, shift=0):
+    """(batch, query head) pairs, ``per_unit`` query heads of each (batch, KV
+    head) unit at different positions of its group (position (u + shift*b) %
+    group, then spread by group / per_unit).  The kernels give each unit its
+    own XCD share (static order) or queue (dynamic schedule), so one head per
+    unit already covers every XCD and every queue of a full-size launch."""
     group = Hq // Hkv
-    return [(b, u * group + (u + shift * b) % group) for b in range(B) for u in range(Hkv)]
+    out = []
+    for b in range(B):
+        for u in range(Hkv):
+            first = (u + shift * b) % group
+            for i in range(per_unit):
+                out.append((b, u * group + (first + i * (group // per_unit)) % group))
+    return out
 
 
 def _oracle_slices(q, k, v, pairs, causal):
-    """fp32 oracle for (batch, query head) pairs, all rows, evaluated on a
-    thread pool (numpy's matmul and exp release the GIL)."""
-    from concurrent.futures import ThreadPoolExecutor
-
-    qn, kn, vn = q.numpy(), k.numpy(), v.numpy()
-
-    def one(bh):
-        b, h = bh
-        return ref.attention_reference_chunked(qn[b:b + 1], kn[b:b + 1], vn[b:b + 1],
-                                               causal=causal, heads=[h], rows=1024,
-                                               return_f32=True)[0, 0]
-
-    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as pool:
-        return list(pool.map(one, pairs))
+    """Unrounded fp32 oracle (the reference's op order with torch on the
+    host CPU, all threads) for (batch, query head) pairs, all rows; a causal
+    row block evaluates only the keys up to its diagonal (the others are
+    hidden from every row of the block)."""
+    out = []
+    for b, h in pairs:
+        out.append(ref.attention_reference_torch_cpu(
+            q[b:b + 1], k[b:b + 1], v[b:b + 1], causal=causal, rows=2048, heads=[h],
+            return_f32=True, skip_hidden=True)[0, 0].numpy())
+    return out
 
 
 def _check_units(q, k, v, out, causal, pairs, label):
@@ -178,10 +181,24 @@ def _check_units(q, k, v, out, causal, pairs, label):
     for (b, h), expect in zip(pairs, _oracle_slices(q, k, v, pairs, causal)):
         res = assert_parity(got[b, h].numpy(), expect, f"{label} b{b} h{h}")
         worst = max(worst, res["max_abs_err"])
-    print(f"  {label}: {len(pairs)} units, worst max_abs={worst:.3e}", flush=True)
+    print(f"  {label}: {len(pairs)} (batch, head) slices, worst max_abs={worst:.3e}", flush=True)
+
+
+def test_heads_per_unit_layout():
+    """The C5 sample holds two distinct heads of every unit, each inside its
+    unit's group; C4's full sample is every head once."""
+    pairs = heads_per_unit(2, 64, 8, per_unit=2, shift=3)
+    assert len(set(pairs)) == 32
+    for b in range(2):
+        for u in range(8):
+            hs = {h for bb, h in pairs if bb == b and h // 8 == u}
+            assert len(hs) == 2
+    assert sorted(h for _, h in heads_per_unit(1, 32, 8, per_unit=4)) == list(range(32))
 
 
 def test_c4_causal_gqa_full_size(device):
+    """C4 at full size: every one of the 32 query heads, every row, against
+    the unrounded fp32 oracle (allclose 2e-3 / 1e-2 and max-abs <= 2e-3)."""
     print("[case] C4 B=1 Hq=32 Hkv=8 N=8192 D=128 causal", flush=True)
     q, k, v = make_inputs(1, 32, 8, 8192, 128, seed=3)
     out = flash_attention_forward(q.to(device), k.to(device), v.to(device), causal=True)
@@ -189,15 +206,15 @@ def test_c4_causal_gqa_full_size(device):
     assert torch.isfinite(out).all().item()
     # causal row 0 attends only to key 0: O[0] == V[kv head][0] exactly
     assert torch.equal(out[0, :, 0].cpu(), v[0].repeat_interleave(4, 0)[:, 0])
-    # one query head of each of the 8 KV heads (0, 5, 10, 15, 16, 21, 26, 31)
-    _check_units(q, k, v, out, True, one_head_per_unit(1, 32, 8), "C4")
+    _check_units(q, k, v, out, True, heads_per_unit(1, 32, 8, per_unit=4), "C4")
 
 
 def test_c5_long_context_stress(device):
     """C5: N(0, 0.5^2) inputs, K x4 on a random 5% of rows (softmax max
-    rescaling stress), B=2 Hq=64 Hkv=8 N=16384 D=128 causal.  One query head
-    of each of the 16 (batch, KV head) units, every row, against the oracle:
-    each unit is one queue of the dynamic schedule this launch runs."""
+    rescaling stress), B=2 Hq=64 Hkv=8 N=16384 D=128 causal.  Two query heads
+    of each of the 16 (batch, KV head) units, at different positions of the
+    unit's group (32 of the 128 slices), every row, against the unrounded fp32
+    oracle: each unit is one queue of the dynamic schedule this launch runs."""
     print("[case] C5 B=2 Hq=64 Hkv=8 N=16384 D=128 causal, K x4 on 5% rows", flush=True)
     g = torch.Generator("cpu").manual_seed(4)
     B, Hq, Hkv, N, D = 2, 64, 8, 16384, 128
@@ -210,7 +227,7 @@ def test_c5_long_context_stress(device):
     torch.cuda.synchronize()
     assert torch.isfinite(out).all().item()
     assert torch.equal(out[:, :, 0].cpu(), v.repeat_interleave(8, 1)[:, :, 0])
-    _check_units(q, k, v, out, True, one_head_per_unit(B, Hq, Hkv, shift=3), "C5")
+    _check_units(q, k, v, out, True, heads_per_unit(B, Hq, Hkv, per_unit=2, shift=3), "C5")
 
 
 def test_warp_softmax_known_answer(device):

@@ -149,6 +149,39 @@ def test_patched_sdpa_matches_fp32_sdpa(device, patched, Nq, Nk, is_causal):
     assert_parity(o, sdpa_ref_cpu(q, k, v, is_causal), f"sdpa Nq{Nq} Nk{Nk}")
 
 
+@pytest.mark.parametrize("mshape", [(2, 1, 1, 40), (24, 40), (24, 24)])
+def test_mask_with_is_causal_behaves_as_unpatched(device, patched, mshape):
+    """A boolean attn_mask together with is_causal=True goes to torch
+    unchanged (reason mask_and_causal; reference examples/
+    llama_attention_replacement.py:61-77 passes every masked call through):
+    the patched call raises the same error as the unpatched one, or, where
+    torch computes the pair, returns what a second unpatched call returns."""
+    nk = mshape[-1]
+    print(f"[case] mask {mshape} with is_causal", flush=True)
+    q = seeded((2, 4, 24, 64), 30).to(device)
+    k = seeded((2, 4, nk, 64), 31).to(device)
+    g = torch.Generator("cpu").manual_seed(32)
+    m = (torch.rand(*mshape, generator=g) < 0.7).to(device)
+    outcome = []
+    for fn in (F.scaled_dot_product_attention, sp._original_sdpa, sp._original_sdpa):
+        try:
+            outcome.append(fn(q, k, k, attn_mask=m, is_causal=True))
+        except RuntimeError as e:
+            outcome.append((type(e).__name__, str(e)))
+    torch.cuda.synchronize()
+    s = sp.patch_stats()
+    assert (s["flash"], s["fallback"], s["fallback_reasons"]) == (0, 1, {"mask_and_causal": 1})
+    kinds = [isinstance(o, tuple) for o in outcome]
+    assert kinds[0] == kinds[1] == kinds[2], outcome
+    if kinds[0]:
+        print(f"  torch raises: {outcome[0][0]}", flush=True)
+        assert outcome[0] == outcome[1] == outcome[2]
+    elif torch.equal(outcome[1], outcome[2]):
+        assert torch.equal(outcome[0], outcome[1])
+    else:  # torch's own call does not repeat; the routing above is the contract
+        print("  torch's own call differs between two runs", flush=True)
+
+
 def test_patched_sdpa_fallbacks(device, patched):
     q = seeded((1, 4, 16, 64), 23).to(device)
     cases = {

@@ -78,6 +78,15 @@ def test_torch_cpu_restatement_matches_numpy():
                                               rows=100).float().numpy()
         # both round the same fp32 value to fp16: at most one ulp apart
         assert np.all(np.abs(a - b) <= np.abs(a) * 2 ** -10 + 2 ** -24)
+        # unrounded, and with a causal block's hidden keys skipped: the fp32
+        # values agree to summation order
+        a32 = ref.attention_reference(q, k, v, causal=causal, return_f32=True)
+        for skip in (False, True):
+            b32 = ref.attention_reference_torch_cpu(
+                torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), causal=causal,
+                rows=100, heads=[2, 0], return_f32=True, skip_hidden=skip)
+            assert b32.dtype == torch.float32
+            np.testing.assert_allclose(b32.numpy(), a32[:, [2, 0]], atol=2e-6, rtol=0)
 
 
 # ---- invariants (closed forms) ---------------------------------------------

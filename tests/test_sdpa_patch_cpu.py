@@ -113,3 +113,36 @@ def test_gqa_without_enable_gqa_raises_like_torch(patched):
         sp._original_sdpa(q, k, k)
     with pytest.raises(RuntimeError):
         F.scaled_dot_product_attention(q, k, k)
+
+
+class _DeviceMask(_DeviceTensor):
+    def __init__(self, *shape):
+        super().__init__(*shape, dtype=torch.bool)
+
+
+def test_mask_with_is_causal_goes_to_torch():
+    """A boolean mask together with is_causal=True is left to torch, which
+    documents the pair as an error (reference examples/
+    llama_attention_replacement.py:61-77 passes every masked call through):
+    the patched call then raises or returns exactly what the unpatched one
+    does.  Either flag alone stays on the kernel."""
+    q = _DeviceTensor(1, 4, 16, 64)
+    m = _DeviceMask(1, 1, 16, 16)
+    assert sp._fallback_reason(q, q, q, m, 0.0, True, {}) == "mask_and_causal"
+    assert sp._fallback_reason(q, q, q, m, 0.0, False, {}) is None
+    assert sp._fallback_reason(q, q, q, None, 0.0, True, {}) is None
+
+
+def test_mask_with_is_causal_on_cpu_matches_unpatched(patched):
+    q = torch.randn(1, 2, 6, 64)
+    m = torch.rand(6, 6) < 0.7
+    outcome = []
+    for fn in (F.scaled_dot_product_attention, sp._original_sdpa):
+        try:
+            outcome.append(fn(q, q, q, attn_mask=m, is_causal=True))
+        except RuntimeError as e:
+            outcome.append((type(e), str(e)))
+    if isinstance(outcome[1], tuple):
+        assert outcome[0] == outcome[1]
+    else:
+        assert torch.equal(outcome[0], outcome[1])

@@ -6,7 +6,8 @@ fa_sm75_workspace_size() bytes: bitwise equal outputs and LSE, on two calls
 in a row where the second is smaller (the scratch keeps the first call's
 contents), for the two paths that use scratch: the split-K decode kernel
 (partials; also with a key-padding mask read as bytes) and the fused
-kernel's dynamic schedule (queue counters).
+kernel's dynamic schedule (queue counters); and a HIP graph whose capture
+holds the process's first noalloc call, replayed against eager calls.
 """
 import ctypes
 
@@ -80,6 +81,65 @@ def assert_same(outs):
     assert torch.equal(o1, o2)
     assert torch.equal(l1, l2)
     assert not torch.isnan(o2).any()
+
+
+def test_first_call_under_graph_capture(device, lib):
+    """The first fa_sm75_forward_noalloc call of the process is made while a
+    HIP graph is being captured (it runs first in this module, and no other
+    test makes a noalloc call that reaches the scratch): the per-device
+    scratch lookup happens inside the capture.  The graph (split-K decode
+    shape: partials in the scratch) is replayed three times on inputs
+    rewritten in place, with eager work between the replays, and each replay
+    is bitwise the eager fa_sm75_forward with a workspace on the same
+    inputs."""
+    B, Hq, Hkv, Nq, Nk, D = 2, 32, 8, 1, 4096, 128
+    print(f"[noalloc graph] B={B} Hq={Hq} Hkv={Hkv} Nq={Nq} Nk={Nk} D={D}", flush=True)
+    q = torch.empty(B, Hq, Nq, D, dtype=torch.float16, device=device)
+    k = torch.empty(B, Hkv, Nk, D, dtype=torch.float16, device=device)
+    v = torch.empty_like(k)
+    o_graph = torch.full_like(q, float("nan"))
+    o_eager = torch.full_like(q, float("nan"))
+
+    def params(o, stream):
+        p = Params()
+        p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+        p.batch, p.heads_q, p.heads_kv, p.seq_len, p.seq_len_kv, p.head_dim = (
+            B, Hq, Hkv, Nq, Nk, D)
+        lib.fa_sm75_set_contiguous_strides(ctypes.byref(p))
+        p.scale, p.stream = D ** -0.5, stream
+        return p
+
+    def fill(seed):
+        g = torch.Generator("cpu").manual_seed(seed)
+        for t in (q, k, v):
+            t.copy_(torch.randn(t.shape, generator=g).half())
+
+    def eager():
+        p = params(o_eager, torch.cuda.current_stream().cuda_stream)
+        need = lib.fa_sm75_workspace_size(ctypes.byref(p))
+        assert need > 0  # the split-K partials
+        ws = torch.empty(need, dtype=torch.uint8, device=device)
+        p.workspace, p.workspace_bytes = ws.data_ptr(), need
+        assert lib.fa_sm75_forward(ctypes.byref(p)) == FA_OK, lib.fa_sm75_last_error()
+        torch.cuda.synchronize()
+        return o_eager.clone()
+
+    fill(1)
+    eager()  # the library's kernels are loaded before the capture
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.fa_sm75_forward_noalloc(
+            ctypes.byref(params(o_graph, torch.cuda.current_stream().cuda_stream)))
+    assert rc == FA_OK, lib.fa_sm75_last_error()
+    for rep in range(3):
+        fill(10 + rep)
+        graph.replay()
+        junk = torch.randn(1 << 20, device=device).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        want = eager()
+        assert torch.isfinite(junk)
+        assert not torch.isnan(o_graph).any()
+        assert torch.equal(o_graph, want), rep
 
 
 def test_split_k_partials_in_scratch(device, lib):
