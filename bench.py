@@ -635,8 +635,10 @@ def main():
     ap.add_argument("--data", default="randn", choices=("randn", "zeros"),
                     help="diagnostic: 'zeros' times the same launches on all-zero inputs "
                          "(the kernel is power-limited: less data toggling, higher clock)")
-    ap.add_argument("--policy", type=int, default=0, choices=(0, 1, 2),
-                    help="kernel policy: 0 auto, 1 = 128-row (4-wave), 2 = 256-row (8-wave)")
+    ap.add_argument("--policy", type=int, default=0, choices=(0, 1, 2, 3, 4, 5),
+                    help="kernel policy: 0 auto, 1 = 128-row (4-wave), 2 = 256-row (8-wave), "
+                         "3 = 128-row dynamic schedule, 4 = key split (8-wave), 5 = paired "
+                         "key split (causal head_dim 64)")
     ap.add_argument("--no-decode", action="store_true",
                     help="skip timing the split-K decode workloads D1-D3")
     ap.add_argument("--no-configs", action="store_true",

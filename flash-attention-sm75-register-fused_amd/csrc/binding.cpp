@@ -439,7 +439,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("abi_version", []() { return fa_sm75_abi_version(); });
   m.def("set_kernel_policy", [](int policy) {
     TORCH_CHECK(fa_sm75_set_kernel_policy(policy) == FA_OK,
-                "kernel policy must be 0 (auto), 1 (narrow), 2 (wide), 3 (dynamic) or 4 (split), got ",
+                "kernel policy must be 0 (auto), 1 (narrow), 2 (wide), 3 (dynamic), 4 (split) or "
+                "5 (split pairs), got ",
                 policy);
   });
   m.def("get_kernel_policy", []() { return fa_sm75_get_kernel_policy(); });

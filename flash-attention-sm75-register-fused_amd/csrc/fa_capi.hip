@@ -189,6 +189,8 @@ fa::FwdArgs make_args(const fa_fwd_params* p) {
   a.ctr = nullptr;
   a.items = 0;
   a.bf16 = p->dtype == FA_DTYPE_BF16 ? 1 : 0;
+  a.pair_half = 0;
+  a.pair_split = 0;
   return a;
 }
 
@@ -499,7 +501,7 @@ int fa_sm75_pack_mask_ranges(const uint8_t* mask, int64_t batch, int64_t heads, 
 }
 
 int fa_sm75_set_kernel_policy(int policy) {
-  if (policy < FA_POLICY_AUTO || policy > FA_POLICY_SPLIT) return FA_ERR_INVALID_ARGUMENT;
+  if (policy < FA_POLICY_AUTO || policy > FA_POLICY_SPLIT_PAIRS) return FA_ERR_INVALID_ARGUMENT;
   g_kernel_policy.store(policy, std::memory_order_relaxed);
   return FA_OK;
 }

@@ -51,9 +51,11 @@ void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int po
       return;
     }
   }
-  if (use_key_split(a, batch, head_dim, causal, policy))
-    launch_shape<8, 0, true, BF16>(a, batch, head_dim, causal, Schedule::kStatic, stream);
-  else
+  if (use_key_split(a, batch, head_dim, causal, policy)) {
+    FwdArgs k = a;
+    k.pair_split = use_pair_split(a, batch, head_dim, causal, policy) ? 1 : 0;
+    launch_shape<8, 0, true, BF16>(k, batch, head_dim, causal, Schedule::kStatic, stream);
+  } else
     launch_shape<4, 0, false, BF16>(a, batch, head_dim, causal, schedule, stream);
 }
 
@@ -110,26 +112,55 @@ int64_t tile_steps_per_head(const FwdArgs& a, bool causal) {
 // neutral at N=8192, 2-5% slower for launches of short items).
 constexpr int64_t kDynamicMinSteps = 1024;
 
-// AUTO takes key-split workgroups at head_dim 128 for causal launches of at
-// most this many 128-row blocks per resident 128-row workgroup, each block
-// row at least kSplitMinBlocks long: every block gets a slot at once, so the
-// largest block's chain of key tiles sets the launch time, and the split
-// halves it.  Measured on MI355X (interleaved A/B against the 4-wave kernel
-// with paired blocks): 16 blocks per row 0.955x, 32 1.02-1.03x, 48-128
-// 1.09x; with more blocks than slots 5-13% slower; at head_dim 64 2-3%
-// slower (its steps are bound by the softmax arithmetic, not the chain).
+// AUTO takes key-split workgroups (8 waves on one 128-row block, one per CU)
+//  * for every launch whose blocks all get a CU at once: there a 4-wave
+//    workgroup would run alone on its CU, one wave per SIMD, where its
+//    steps are bound by latency; two waves per SIMD on half the key tiles
+//    each finish the block sooner.  Measured on MI355X (interleaved A/B
+//    against AUTO's 4-wave kernel, head_dim 64 and 128, full and causal,
+//    B=1 H=8 N=2048/4096 and B=1 H=32 N=512/1024): 1.02-1.22x;
+//  * at head_dim 128 for causal launches of at most this many 128-row
+//    blocks per resident 128-row workgroup, each block row at least
+//    kSplitMinBlocks long: the largest block's chain of key tiles sets the
+//    launch time, and the split halves it (16 blocks per row 0.955x, 32
+//    1.02-1.03x, 48-128 1.09x; with more blocks than slots 5-13% slower).
+// Causal head_dim-64 launches whose blocks outnumber the CUs but whose pairs
+// of blocks (block i with block nqb-1-i of the same head) do not, with rows
+// of at least kSplitMinBlocks blocks, run the paired key split instead: one
+// round of 8-wave workgroups, each pair's key tiles dealt evenly to the two
+// groups (B=1 H=16 N=4096: 1.055x).  With shorter rows the 4-wave kernel's
+// large/small block pairing on one CU does as well (C3, 16 blocks per row:
+// 0.98x paired key split).  Two waves of one workgroup on a SIMD stop at the
+// same barriers, and at head_dim 64 a step is bound by its VALU work (the
+// 32 exponentials and the fp16 packing, row max and sum of 2048 scores per
+// wave), which two waves on a SIMD share: a SIMD runs one 64-key step of
+// two waves in about as many cycles as two steps of one.
 constexpr int64_t kSplitMaxItems = 1;
 constexpr int kSplitMinBlocks = 32;
 
+int64_t compute_units() { return resident_fused_workgroups() / 2; }
+
 }  // namespace
+
+bool use_pair_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy) {
+  if (has_mask(a) || !causal || head_dim != 64) return false;
+  if (policy == 5) return true;
+  if (policy != 0) return false;
+  FwdArgs planned = a;
+  if (plan_grid(planned, batch, 128) <= compute_units()) return false;  // plain key split
+  if (planned.num_qblocks < kSplitMinBlocks) return false;
+  return plan_pairs(planned, batch) <= compute_units();
+}
 
 bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy) {
   if (has_mask(a)) return false;
-  if (policy == 4) return true;
-  if (policy != 0 || !causal || head_dim != 128) return false;
+  if (policy == 4 || policy == 5) return true;
+  if (policy != 0) return false;
   FwdArgs planned = a;
   plan_grid(planned, batch, 128);
-  return planned.num_qblocks >= kSplitMinBlocks &&
+  if (planned.items <= compute_units()) return true;
+  if (use_pair_split(a, batch, head_dim, causal, policy)) return true;
+  return causal && head_dim == 128 && planned.num_qblocks >= kSplitMinBlocks &&
          planned.items <= kSplitMaxItems * resident_fused_workgroups();
 }
 

@@ -90,6 +90,20 @@ namespace {
 // tail (measured: C3 +3.4%, B=1 Hq=14 Hkv=2 N=4096 +4.8%; launches that keep
 // two waves per SIMD busy throughout lose 1-2%, the extra matrix work costing
 // clock).
+// LDS through which group 1 of a paired key split hands its share of block A
+// to group 0: per row wave, MT * 1024 floats of O (four consecutive floats of
+// a lane's accumulator per 16-byte slot), then 64 running maxima and 64 lane
+// partial sums.  Only the instances that run pairs allocate it.
+template <bool P, int MT>
+__device__ __forceinline__ float* pair_exchange() {
+  if constexpr (P) {
+    __shared__ __attribute__((aligned(16))) float xo[4 * (MT * 1024 + 128)];
+    return xo;
+  } else {
+    return nullptr;
+  }
+}
+
 template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, int MASK_MODE, bool KSPLIT, bool BF16,
           bool ROWSUM>
 __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
@@ -110,6 +124,9 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   constexpr int SEGQ = L::Segs / 4;               // segments of one tile per wave quarter
   constexpr int LPW = 2 * L::Segs / ROW_WAVES;    // direct loads per wave per step
   constexpr bool SPLIT_ROLES = WAVES == 8 && !KSPLIT;  // a wave loads K or V, not both
+  // The paired key split (a.pair_split) runs on the head_dim-64 causal
+  // key-split instances (the head_dim-128 ones fill the LDS already).
+  constexpr bool PAIRS = KSPLIT && D == 64 && CAUSAL;
   static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
   static_assert(!KSPLIT || (WAVES == 8 && !MASK), "key split: 8 waves, no mask");
   static_assert(L::Segs % 4 == 0, "tile segments must split over 4 waves");
@@ -220,14 +237,32 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     const bool prefetch = dynamic && !((empty_q >> own_q) & 1u);
     uint64_t next_claim = 0ull;
 
-    const Work w = block_work(a, item, CAUSAL);
-    const int b = w.b, hq = w.hq, hkv = w.hkv, qb = w.qb;
+    // Paired key split (KSPLIT at head_dim 64 with a.pair_split): the work
+    // item is a pair of query blocks of one (batch, head), A = block nqb-1-i
+    // and B = block i (none when the two coincide, the middle block of an odd
+    // count), so under causal masking A is the larger.  Their T_A + T_B key
+    // tiles are dealt evenly to the two key groups: group 0 runs tiles
+    // [0, h) of A and group 1 the rest of A, then all of B, h = ceil((T_A +
+    // T_B) / 2), both h steps.  Group 1 hands its share of A (unnormalised O,
+    // running max, partial sums) to group 0 through LDS when it moves on to B;
+    // group 0 merges it at the end and stores A, group 1 stores B.  Tile
+    // indices in the step loop are then virtual (group 1 counts on from h):
+    // tile_of maps them to key tiles, and seg_b tells B's from A's.
+    const bool pairs = PAIRS && a.pair_split != 0;
+    const Work w = block_work(a, item, CAUSAL && !pairs);
+    const int b = w.b, hq = w.hq, hkv = w.hkv;
+    const int N = a.n;    // query rows
+    const int NK = a.nk;  // key rows
+    const int nqb = (N + BLOCK_M - 1) / BLOCK_M;
+    const int qb = pairs ? nqb - 1 - w.qb : w.qb;
+    const int qb_b = pairs && w.qb < nqb - 1 - w.qb ? w.qb : -1;  // block B, or -1
     const int bh = b * a.hq + hq;
     const int q0 = qb * BLOCK_M;
     const int qw = q0 + rw * 32;
     const int qrow = qw + ql;
-    const int N = a.n;    // query rows
-    const int NK = a.nk;  // key rows
+    const int qw_b = qb_b * BLOCK_M + rw * 32;  // (pairs with a block B)
+    const int qrow_b = qw_b + ql;
+    const bool g1b = pairs && kgrp == 1 && qb_b >= 0;  // this group moves on to B
 
     const _Float16* Qp = a.q + b * a.qsb + hq * a.qsh;
     // Mask bits of this lane's query row (rows past N read row N - 1), or
@@ -249,19 +284,27 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     const _Float16* Kp = a.k + b * a.ksb + hkv * a.ksh;
     const _Float16* Vp = a.v + b * a.vsb + hkv * a.vsh;
 
-    // Q^T fragments (B operand of S^T = K Q^T), resident for the whole kernel.
+    // Q^T fragments (B operand of S^T = K Q^T), resident for the whole kernel
+    // (in pair mode group 1 also holds B's, which replace A's when it moves on).
+    auto load_q = [&](int row, half8 (&qd)[KK]) {
+      if (row < N) {
+        const _Float16* qp = Qp + (int64_t)row * a.qsn + 8 * hi;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) qd[kk] = *(const half8*)(qp + 16 * kk);
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) qd[kk] = (half8)(_Float16)0;
+      }
+      if (a.negate_q) {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) qd[kk] = negate16(qd[kk]);
+      }
+    };
     half8 qf[KK];
-    if (qrow < N) {
-      const _Float16* qp = Qp + (int64_t)qrow * a.qsn + 8 * hi;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) qf[kk] = *(const half8*)(qp + 16 * kk);
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) qf[kk] = (half8)(_Float16)0;
-    }
-    if (a.negate_q) {
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) qf[kk] = negate16(qf[kk]);
+    half8 qf_b[PAIRS ? KK : 1];
+    load_q(qrow, qf);
+    if constexpr (PAIRS) {
+      if (g1b) load_q(qrow_b, qf_b);
     }
 
     // Mask ranges (mask bits with a.mranges): the span of keys some row of
@@ -300,13 +343,29 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // Keys this block can see (none for a block entirely before the diagonal).
     const int kv_len = min(CAUSAL ? max(0, min(NK, q0 + BLOCK_M + a.diag)) : NK, span_hi);
     const int block_tiles = (kv_len + kBlockN - 1) / kBlockN;
+    // Key tiles of block B (pair mode; 0 without one).
+    const int kv_len_b =
+        qb_b >= 0 ? (CAUSAL ? max(0, min(NK, qb_b * BLOCK_M + BLOCK_M + a.diag)) : NK) : 0;
+    const int tiles_b = (kv_len_b + kBlockN - 1) / kBlockN;
     const int first_tile = span_lo < span_hi ? span_lo / kBlockN : 0;
     // Tiles [tile0, tile0 + ntiles) of this wave's key group.  KSPLIT: both
-    // groups run ceil(block_tiles / 2) steps (so their barriers pair up); a
-    // tile past the block's keys is fully masked and adds exactly nothing.
-    const int ntiles = KSPLIT ? (block_tiles + 1) / 2 : max(0, block_tiles - first_tile);
+    // groups run ceil((block_tiles + tiles_b) / 2) steps (so their barriers
+    // pair up); a tile past the block's keys is fully masked and adds
+    // exactly nothing.
+    const int ntiles =
+        KSPLIT ? (block_tiles + tiles_b + 1) / 2 : max(0, block_tiles - first_tile);
     const int tile0 = KSPLIT ? kgrp * ntiles : first_tile;
     const int tile_end = tile0 + ntiles;
+    // Virtual tile j (pair mode): B's tile j - T_A once j reaches T_A.
+    auto seg_b = [&](int j) { return PAIRS && qb_b >= 0 && j >= block_tiles; };
+    auto tile_of = [&](int j) { return seg_b(j) ? j - block_tiles : j; };
+    // Group 1 starting directly in B holds B's Q from the start.
+    if constexpr (PAIRS) {
+      if (g1b && tile0 >= block_tiles) {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) qf[kk] = qf_b[kk];
+      }
+    }
 
     // Direct-load map: wave quarter wq fills 1 KB segments wq, wq + 4, ... of a
     // tile; lane l of a segment covers tile bytes [1024 seg + 16 l, +16).  The
@@ -357,12 +416,15 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       asm volatile("" : "+s"(off));
       return (lds_void*)(tile + off);
     };
-    // Buffer windows of tile j (empty past the last tile: every lane reads 0).
-    auto k_window = [&](int j) {
+    // Buffer windows of (virtual) tile jv (empty past the last tile: every
+    // lane reads 0).
+    auto k_window = [&](int jv) {
+      const int j = tile_of(jv);
       const int bytes = k_all_bytes - j * k_tile_bytes;
       return make_rsrc(Kp + (int64_t)j * kBlockN * a.ksn, bytes > 0 ? bytes : 0);
     };
-    auto v_window = [&](int j) {
+    auto v_window = [&](int jv) {
+      const int j = tile_of(jv);
       const int bytes = v_all_bytes - j * v_tile_bytes;
       return make_rsrc(Vp + (int64_t)j * kBlockN * a.vsn, bytes > 0 ? bytes : 0);
     };
@@ -433,6 +495,30 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // score exceeds thr = m_run + kRescaleLog2 / c2 (-inf before any key).
     float thr = -__builtin_inff();
 
+    // Pair mode, group 1: its share of block A (unnormalised O, running max,
+    // lane partial sums) into the exchange area for group 0, and a fresh
+    // state for block B.
+    float* const pair_xo = pair_exchange<PAIRS, MT>() + (PAIRS ? rw * (MT * 1024 + 128) : 0);
+    auto hand_off_a = [&]() {
+      if constexpr (PAIRS) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *(float4*)(pair_xo + ((mt * 4 + g) * 64 + lane) * 4) =
+                float4{oacc[mt][4 * g], oacc[mt][4 * g + 1], oacc[mt][4 * g + 2],
+                       oacc[mt][4 * g + 3]};
+        pair_xo[MT * 1024 + lane] = m_run;
+        pair_xo[MT * 1024 + 64 + lane] = l_run;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) oacc[mt] = (float16v)0.0f;
+        m_run = -__builtin_inff();
+        l_run = 0.0f;
+        mc = 0.0f;
+        thr = -__builtin_inff();
+      }
+    };
+
     // Prepares tile j's scores for its softmax: masks them if tile j crosses
     // the sequence end or this wave's causal diagonal, or (MASK) hides a key
     // from some row of the wave (the unmasked max mx is then recomputed),
@@ -443,17 +529,20 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // no exchange between them, the rare rescale does).  mw: the lane's mask
     // word of tile j (bit k: key 64 j + k visible), or its key byte (key-padding
     // bytes), from which the wave's ballot forms that word.
-    auto prepare = [&](int j, float16v (&s)[2], float mx, uint64_t mw) {
+    auto prepare = [&](int jv, float16v (&s)[2], float mx, uint64_t mw) {
       if constexpr (KEY_BYTES) mw = __builtin_amdgcn_ballot_w64(mw != 0);
-      const int kstart = j * kBlockN;
+      const int kstart = tile_of(jv) * kBlockN;
+      const bool in_b = seg_b(jv);
+      const int qw_j = in_b ? qw_b : qw;
+      const int qrow_j = in_b ? qrow_b : qrow;
       bool need_mask =
-          (kstart + kBlockN > NK) || (CAUSAL && kstart + kBlockN - 1 > qw + a.diag);
+          (kstart + kBlockN > NK) || (CAUSAL && kstart + kBlockN - 1 > qw_j + a.diag);
       if (MASK) need_mask = need_mask || __builtin_amdgcn_ballot_w64(~mw != 0) != 0;
       if (need_mask) {
         const uint64_t mws = mw >> (4 * hi);  // bit 32 t + 8 (i / 4) + i % 4: element (t, i)
         // Element (t, i) holds key kstart + 4 hi + off, off = 32 t + 8 (i / 4)
         // + i % 4 (a constant); it is visible iff off <= lim.
-        const int last = CAUSAL ? min(NK - 1, qrow + a.diag) : NK - 1;
+        const int last = CAUSAL ? min(NK - 1, qrow_j + a.diag) : NK - 1;
         const int lim = last - kstart - 4 * hi;
         // static_for: a loop the unroller leaves rolled would index s at run
         // time and move the score registers to scratch memory.
@@ -581,6 +670,13 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       // workgroup's wave on the SIMD while that one runs prepare / waits at its
       // barrier (measured +1% on C4, +0.3% on C5; at head_dim 64, whose steps
       // are VALU-bound, -2%, so not there).
+      // Pair mode, group 1: S_{j+1} is B's first tile.
+      if constexpr (PAIRS) {
+        if (HAS_NEXT && g1b && j + 1 == block_tiles) {
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) qf[kk] = qf_b[kk];
+        }
+      }
       if constexpr (D == 128) __builtin_amdgcn_s_setprio(1);
       static_for<(PFK < ns ? PFK : ns)>([&](auto i_c) {
         kf[decltype(i_c)::value] = read_k(Kn, decltype(i_c)::value);
@@ -631,6 +727,10 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       });
 
       if constexpr (D == 128) __builtin_amdgcn_s_setprio(0);
+      // Pair mode, group 1: P_j V_j was A's last tile.
+      if constexpr (PAIRS) {
+        if (g1b && j + 1 == block_tiles) hand_off_a();
+      }
       if (HAS_NEXT) {
         prepare(j + 1, s_nxt, mx_next, mw_next);
         // The loads of the previous step have landed (those of this step may
@@ -640,6 +740,10 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       }
     };
 
+    // Pair mode, group 1 with no tile of A: its (empty) share of A.
+    if constexpr (PAIRS) {
+      if (g1b && tile0 >= block_tiles) hand_off_a();
+    }
     // ---- prologue: K_0..K_{STAGES-1} and V_0..V_{STAGES-2} into LDS; S_0 -----
     // (tile indices relative to tile0)
     if (ntiles > 0) {
@@ -698,12 +802,14 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     if constexpr (KSPLIT) {
       // Group 1 wave w+4 hands its O (unnormalised), running max and partial
       // sums to group 0 wave w (same rows, same lane layout) through the
-      // group-1 half of one LDS array, which no wave reads any more.
+      // group-1 half of one LDS array, which no wave reads any more (pair
+      // mode: the exchange area, which a group 1 that moved on to block B
+      // filled already).
       __syncthreads();
       _Float16* const arr = rw == 0 ? k_lds0 : rw == 1 ? k_lds1 : rw == 2 ? v_lds0 : v_lds1;
-      float* const xo = (float*)(arr + L::Tile);
+      float* const xo = pairs ? pair_xo : (float*)(arr + L::Tile);
       static_assert(MT * 16 * 64 * 4 + 2 * 64 * 4 <= L::Tile * 2, "exchange fits a tile");
-      if (kgrp == 1) {
+      if (kgrp == 1 && !g1b) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -740,10 +846,12 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     }
 
     // ---- epilogue: combine the two half-wave partial sums, normalise, store ---
+    // (pair mode: group 0 stores block A, a group 1 that moved on stores B)
     const float l_tot = halves_sum(l_run);
     const float inv = (l_tot > 0.0f) ? (1.0f / l_tot) : 0.0f;
-    if (qrow < N && kgrp == 0) {
-      _Float16* op = a.o + b * a.osb + hq * a.osh + (int64_t)qrow * a.osn;
+    const int srow = g1b ? qrow_b : qrow;
+    if (srow < N && (kgrp == 0 || g1b)) {
+      _Float16* op = a.o + b * a.osb + hq * a.osh + (int64_t)srow * a.osn;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -757,7 +865,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       if (a.lse != nullptr && hi == 0) {
         const float m_use = (m_run == -__builtin_inff()) ? 0.0f : m_run;
         const float lse2 = m_use * c2 + __builtin_log2f(l_tot);
-        a.lse[(int64_t)bh * N + qrow] = lse2 * 0.69314718055994530942f;
+        a.lse[(int64_t)bh * N + srow] = lse2 * 0.69314718055994530942f;
       }
     }
     if (!dynamic) break;
@@ -782,7 +890,9 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream) {
   const bool same = a.ksn == a.vsn;
   FwdArgs args = a;
-  int64_t wgs = plan_grid(args, batch, KSPLIT ? 128 : 32 * WAVES);
+  int64_t wgs = KSPLIT && D == 64 && causal && a.pair_split != 0
+                    ? plan_pairs(args, batch)
+                    : plan_grid(args, batch, KSPLIT ? 128 : 32 * WAVES);
   const int64_t slots = resident_fused_workgroups();
   if (WAVES == 4 && args.ctr != nullptr && use_dynamic_schedule(args, batch, causal, schedule)) {
     launch_clear_tickets(args.ctr, stream);

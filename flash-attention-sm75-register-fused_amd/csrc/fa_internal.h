@@ -41,6 +41,7 @@ struct FwdArgs {
   int items;        // work items (query blocks): filled by the launcher
   int bf16;         // elements are bfloat16 (else binary16)
   int pair_half;    // > 0: single-round causal order pairing (launcher; block_work)
+  int pair_split;   // 1: key-split workgroups take pairs of query blocks (launcher)
 };
 
 // Whether a call carries an explicit mask (bits or key-padding bytes): the
@@ -81,6 +82,17 @@ inline int64_t plan_grid(FwdArgs& a, int batch, int block_m) {
   a.xcds = a.units % kNumXcds == 0 ? kNumXcds : 1;
   a.items = batch * a.hq * a.num_qblocks;
   a.pair_half = 0;
+  a.pair_split = 0;
+  return a.items;
+}
+// Plan of the paired key split: work item = a pair of query blocks of one
+// (batch, query head), ceil(num_qblocks / 2) per head (128-row blocks);
+// returns the number of items.
+inline int64_t plan_pairs(FwdArgs& a, int batch) {
+  plan_grid(a, batch, 128);
+  a.num_qblocks = (a.num_qblocks + 1) / 2;
+  a.items = batch * a.hq * a.num_qblocks;
+  a.pair_split = 1;
   return a.items;
 }
 // Whether the 4-wave kernel runs the dynamic schedule for a planned call
@@ -97,9 +109,15 @@ int64_t fused_workspace_bytes(const FwdArgs& a, int batch, int head_dim, bool ca
 template <int D, int WAVES, int MASK, bool KSPLIT, bool BF16>
 void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream);
-// Whether a call runs on key-split workgroups: policy 4, or AUTO for causal
-// head_dim-128 launches whose time is set by their largest query block.
+// Whether a call runs on key-split workgroups: policy 4 or 5, or AUTO for
+// launches whose blocks (or, causal at head_dim 64, pairs of blocks) all
+// get a CU at once, and for causal head_dim-128 launches whose time is set
+// by their largest query block.
 bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy);
+// Whether key-split workgroups take pairs of query blocks (causal head_dim
+// 64: policy 5, or AUTO when the blocks outnumber the CUs but the pairs do
+// not, in rows of at least 32 blocks).
+bool use_pair_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy);
 int fused_block_m();  // rows of the smallest workgroup (grid-size checks)
 
 // Split-K path (fa_decode.hip): taken when heads_q / heads_kv * seq_len <=

@@ -203,23 +203,29 @@ int fa_sm75_abi_version(void);
 
 /* Fused-kernel selection, process-wide (no reference counterpart: a tuning
  * and testing control).  AUTO picks by problem size: the split-K path for
- * few query rows per K/V head; key-split workgroups for causal head_dim-128
- * launches small enough that their largest query block sets their time;
- * else 128-row workgroups, with the dynamic XCD-balanced schedule for long
- * launches when p->workspace holds its counters.  NARROW forces 128-row
- * workgroups of 4 waves (two per CU) on the static schedule (one workgroup
- * per query block); WIDE forces 256-row workgroups of 8 waves (one per CU,
- * K/V tiles triple-buffered); DYNAMIC forces 128-row workgroups on the
- * dynamic schedule whenever the workspace holds its counters; SPLIT forces
- * 128-row workgroups of 8 waves, two groups of 4 each taking half of the
- * block's key tiles (one per CU).  All compute the same function (the two
- * schedules bitwise so). */
+ * few query rows per K/V head; key-split workgroups for launches whose
+ * query blocks all get a CU at once and for causal head_dim-128 launches
+ * small enough that their largest query block sets their time; paired
+ * key-split workgroups for causal head_dim-64 launches whose pairs of query
+ * blocks all get a CU at once (rows of at least 32 blocks); else 128-row workgroups, with the dynamic
+ * XCD-balanced schedule for long launches when p->workspace holds its
+ * counters.  NARROW forces 128-row workgroups of 4 waves (two per CU) on
+ * the static schedule (one workgroup per query block); WIDE forces 256-row
+ * workgroups of 8 waves (one per CU, K/V tiles triple-buffered); DYNAMIC
+ * forces 128-row workgroups on the dynamic schedule whenever the workspace
+ * holds its counters; SPLIT forces 128-row workgroups of 8 waves, two
+ * groups of 4 each taking half of the block's key tiles (one per CU);
+ * SPLIT_PAIRS forces, for causal head_dim-64 calls (else as SPLIT),
+ * workgroups of 8 waves on query blocks i and nqb-1-i of one head, their key
+ * tiles dealt evenly to the two groups.  All compute the same function (the
+ * two schedules bitwise so). */
 enum fa_kernel_policy {
   FA_POLICY_AUTO = 0,
   FA_POLICY_NARROW = 1,
   FA_POLICY_WIDE = 2,
   FA_POLICY_DYNAMIC = 3,
-  FA_POLICY_SPLIT = 4
+  FA_POLICY_SPLIT = 4,
+  FA_POLICY_SPLIT_PAIRS = 5
 };
 int fa_sm75_set_kernel_policy(int policy); /* FA_OK or FA_ERR_INVALID_ARGUMENT */
 int fa_sm75_get_kernel_policy(void);

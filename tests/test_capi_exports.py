@@ -172,7 +172,7 @@ def test_workspace_size(lib):
     assert lib.fa_sm75_workspace_size(ctypes.byref(short_call)) == 0
     lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
     try:
-        for policy, want in ((1, 0), (2, 0), (3, 8 * 256), (4, 0)):
+        for policy, want in ((1, 0), (2, 0), (3, 8 * 256), (4, 0), (5, 0)):
             lib.fa_sm75_set_kernel_policy(policy)
             assert lib.fa_sm75_workspace_size(ctypes.byref(p)) == want, policy
             assert lib.fa_sm75_workspace_size(ctypes.byref(long_call)) == want, policy
@@ -271,10 +271,10 @@ def test_abi_version(lib):
 def test_kernel_policy_switch(lib):
     lib.fa_sm75_set_kernel_policy.argtypes = [ctypes.c_int]
     assert lib.fa_sm75_get_kernel_policy() == 0
-    assert lib.fa_sm75_set_kernel_policy(5) == 1
+    assert lib.fa_sm75_set_kernel_policy(6) == 1
     assert lib.fa_sm75_set_kernel_policy(-1) == 1
     try:
-        for p in (1, 2, 3, 4, 0):
+        for p in (1, 2, 3, 4, 5, 0):
             assert lib.fa_sm75_set_kernel_policy(p) == 0
             assert lib.fa_sm75_get_kernel_policy() == p
     finally:

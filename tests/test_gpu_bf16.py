@@ -111,7 +111,7 @@ def test_bf16_kernels_agree(device):
     qd, kd, vd = q.to(device), k.to(device), v.to(device)
     outs = {}
     try:
-        for pol in (0, 1, 3, 4):  # auto, 128-row static, dynamic, key split
+        for pol in (0, 1, 3, 4, 5):  # auto, 128-row static, dynamic, key split, pairs
             _C.set_kernel_policy(pol)
             outs[pol] = flash_attention_forward_ex(qd, kd, vd, causal=True)
     finally:
