@@ -208,7 +208,7 @@ __global__ void __launch_bounds__(512, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
         for (int h = 0; h < heads; ++h) {
           const int32_t* rr = a.mranges + 2 * (b * a.mrsb + (int64_t)(hkv * a.group + h) * a.mrsh +
                                                (int64_t)r * a.mrsq);
-          if (rr[0] < k0 + kBwdBlockKeys && rr[1] > k0) {
+          if (range_first_key(rr[0]) < k0 + kBwdBlockKeys && rr[1] > k0) {
             lo = min(lo, r);
             hi = max(hi, r + 1);
           }
@@ -661,7 +661,7 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
     if (a.mranges != nullptr) {
       const int32_t* rr =
           a.mranges + 2 * (b * a.mrsb + hq * a.mrsh + (int64_t)min(qrow, N - 1) * a.mrsq);
-      span_lo = rr[0];
+      span_lo = range_first_key(rr[0]);
       span_hi = rr[1];
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {

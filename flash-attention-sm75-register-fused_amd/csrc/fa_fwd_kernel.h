@@ -155,7 +155,8 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   // Work items.  Static schedule (a.ctr == nullptr): workgroup wg does item
   // wg.  Dynamic schedule (4-wave kernel, a.ctr set, grid = resident
   // workgroups): the items form a.xcds queues, queue x holding the items the
-  // static schedule gives XCD x, in the same (largest first) order.  A
+  // static schedule gives XCD x, one (batch, KV head) unit after the other
+  // and largest first within each (block_work's unit_major order).  A
   // workgroup takes items from the head of its own XCD's queue; once that is
   // empty it takes from the tail (the smallest items) of the others, so XCDs
   // running at a higher clock take over the end of slower XCDs' work
@@ -249,7 +250,10 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // indices in the step loop are then virtual (group 1 counts on from h):
     // tile_of maps them to key tiles, and seg_b tells B's from A's.
     const bool pairs = PAIRS && a.pair_split != 0;
-    const Work w = block_work(a, item, CAUSAL && !pairs);
+    // Mask ranges make the blocks' work uneven like a causal launch's (a
+    // causal mask given as bits): the same largest-first order then.
+    const bool big_first = CAUSAL || (MASK && !KEY_BYTES && a.mranges != nullptr);
+    const Work w = block_work(a, item, big_first && !pairs, dynamic);
     const int b = w.b, hq = w.hq, hkv = w.hkv;
     const int N = a.n;    // query rows
     const int NK = a.nk;  // key rows
@@ -313,13 +317,30 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // reads its row's pair (rows past N read row N - 1), the wave and then
     // the workgroup (through V_1's buffer, which no load writes before step
     // 0) take the union.
+    // Dense waves: when every row of the wave sees exactly the interval of
+    // its pair (bit 31 of the first entry), the keys [in_lo, in_hi) are
+    // visible to all of them, and a tile inside that span needs no mask word
+    // (it would be all ones; the sequence end and the causal diagonal are
+    // masked as without a mask).  in_hi <= in_lo: no such tile.
     int span_lo = 0, span_hi = NK;
+    int in_lo = 0, in_hi = 0;
     if constexpr (MASK && !KEY_BYTES) {
       if (a.mranges != nullptr) {
         const int32_t* rr =
             a.mranges + 2 * (b * a.mrsb + hq * a.mrsh + (int64_t)min(qrow, N - 1) * a.mrsq);
-        span_lo = rr[0];
+        const int32_t first = rr[0];
+        span_lo = range_first_key(first);
         span_hi = rr[1];
+        int lo_max = span_lo, hi_min = span_hi;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          lo_max = max(lo_max, __shfl_xor(lo_max, d));
+          hi_min = min(hi_min, __shfl_xor(hi_min, d));
+        }
+        if (__builtin_amdgcn_ballot_w64(!range_is_dense(first)) == 0) {
+          in_lo = __builtin_amdgcn_readfirstlane(lo_max);
+          in_hi = __builtin_amdgcn_readfirstlane(hi_min);
+        }
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
           span_lo = min(span_lo, __shfl_xor(span_lo, d));
@@ -340,6 +361,12 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         span_hi = __builtin_amdgcn_readfirstlane(span_hi);
       }
     }
+    // The mask word (or key byte) prepare takes for tile j: none to load for
+    // a tile every row of a dense wave sees in full.
+    auto mask_word = [&](int j) -> uint64_t {
+      if (j * kBlockN >= in_lo && j * kBlockN + kBlockN <= in_hi) return ~0ull;
+      return mask_ahead(j);
+    };
     // Keys this block can see (none for a block entirely before the diagonal).
     const int kv_len = min(CAUSAL ? max(0, min(NK, q0 + BLOCK_M + a.diag)) : NK, span_hi);
     const int block_tiles = (kv_len + kBlockN - 1) / kBlockN;
@@ -597,7 +624,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       if (HAS_NEXT) {
         rk_next = k_window(j + STAGES);
         rv_next = v_window(j + STAGES - 1);
-        if (MASK) mw_next = mask_ahead(j + 1);  // consumed by prepare(j + 1) at the end
+        if (MASK) mw_next = mask_word(j + 1);  // consumed by prepare(j + 1) at the end
       }
       _Float16* k_dst = kbuf(std::integral_constant<int, U>{});
       _Float16* v_dst = vbuf(std::integral_constant<int, U + STAGES - 1>{});
@@ -764,7 +791,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         for (int kk = 0; kk < KK; ++kk)
           s_buf[0][t] = E::mfma(read_k(k_first, t * KK + kk), qf[kk], s_buf[0][t]);
       }
-      prepare(tile0, s_buf[0], row_max(s_buf[0]), MASK ? mask_ahead(tile0) : ~0ull);
+      prepare(tile0, s_buf[0], row_max(s_buf[0]), MASK ? mask_word(tile0) : ~0ull);
       // Step 0 loads K_STAGES into K_0's buffer: every wave must be done
       // reading it for S_0 first.
       __syncthreads();

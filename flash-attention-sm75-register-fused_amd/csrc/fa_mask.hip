@@ -19,6 +19,13 @@
 //
 // Other key strides: one wave builds one word per iteration, lane k reading
 // element 64 w + k of the row, and a ballot over the wave is the word.
+//
+// Ranges (fa_sm75_pack_mask_ranges): each row's first visible key and one
+// past its last, with bit 31 of the first set when every key between them
+// is visible (the row's visible keys are exactly that interval: a causal,
+// padding or sliding-window row).  The forward kernel then knows, without
+// reading a mask word, that a tile inside the interval of every row of a
+// wave hides nothing.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -51,13 +58,21 @@ __device__ __forceinline__ void add_span(int& lo, int& hi, int k0, uint32_t bits
   }
 }
 
-// The wave's span (every lane gets it).
-__device__ __forceinline__ void reduce_span(int& lo, int& hi) {
+// The wave's span and count of visible keys (every lane gets them).
+__device__ __forceinline__ void reduce_span(int& lo, int& hi, int& cnt) {
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     lo = min(lo, __shfl_xor(lo, d));
     hi = max(hi, __shfl_xor(hi, d));
+    cnt += __shfl_xor(cnt, d);
   }
+}
+
+// The first entry of a row's range pair: its first visible key, bit 31 set
+// when all keys of [lo, hi) are visible.
+__device__ __forceinline__ int32_t range_first(int lo, int hi, int cnt, int64_t cols) {
+  if (hi <= 0) return (int32_t)cols;  // no visible key
+  return cnt == hi - lo ? (int32_t)((uint32_t)lo | 0x80000000u) : lo;
 }
 
 // Packs chunks c .. c + PASS - 1 (1024 bytes each) of the row at rp into out
@@ -66,7 +81,7 @@ __device__ __forceinline__ void reduce_span(int& lo, int& hi) {
 template <int PASS, bool RANGES>
 __device__ __forceinline__ void pack_chunks(const uint8_t* rp, int64_t c, int64_t cols,
                                             int64_t words, uint64_t* row_out, int lane, int& lo,
-                                            int& hi) {
+                                            int& hi, int& cnt) {
   u32x4 v[PASS];
   bool whole[PASS];
 #pragma unroll
@@ -86,7 +101,10 @@ __device__ __forceinline__ void pack_chunks(const uint8_t* rp, int64_t c, int64_
       for (int e = 0; e < 16; ++e)
         if (k0 + e < cols && rp[k0 + e] != 0) bits |= 1u << e;
     }
-    if constexpr (RANGES) add_span(lo, hi, (int)k0, bits);
+    if constexpr (RANGES) {
+      add_span(lo, hi, (int)k0, bits);
+      cnt += __builtin_popcount(bits);
+    }
     // Word j of this chunk: the 16-bit groups of lanes 4j .. 4j + 3.
     const uint64_t g0 = (uint32_t)__shfl((int)bits, 4 * lane);
     const uint64_t g1 = (uint32_t)__shfl((int)bits, 4 * lane + 1);
@@ -113,18 +131,18 @@ __global__ void __launch_bounds__(64 * kPackWaves) fa_pack_mask_rows_kernel(
     const int64_t i = row % rows;
     const int64_t bh = row / rows;
     const uint8_t* rp = mask + (bh / heads) * sb + (bh % heads) * sh + i * sq;
-    int lo = (int)cols, hi = 0;
+    int lo = (int)cols, hi = 0, cnt = 0;
     if constexpr (RANGES) {
       for (int64_t sp = 0; sp < spans; ++sp)
-        pack_chunks<PASS, true>(rp, sp * PASS, cols, words, out + row * words, lane, lo, hi);
-      reduce_span(lo, hi);
+        pack_chunks<PASS, true>(rp, sp * PASS, cols, words, out + row * words, lane, lo, hi, cnt);
+      reduce_span(lo, hi, cnt);
       if (lane == 0) {
-        ranges[2 * row] = hi > 0 ? lo : (int)cols;
+        ranges[2 * row] = range_first(lo, hi, cnt, cols);
         ranges[2 * row + 1] = hi;
       }
     } else {
       pack_chunks<PASS, false>(rp, (it - row * spans) * PASS, cols, words, out + row * words,
-                               lane, lo, hi);
+                               lane, lo, hi, cnt);
     }
   }
 }
@@ -146,7 +164,7 @@ __global__ void __launch_bounds__(64 * kPackWaves) fa_pack_mask_kernel(
     const uint8_t* rp = mask + (bh / heads) * sb + (bh % heads) * sh + i * sq;
     const int64_t w0 = RANGES ? 0 : it - row * words;
     const int64_t w1 = RANGES ? words : w0 + 1;
-    int lo = (int)cols, hi = 0;  // wave-uniform (from ballots)
+    int lo = (int)cols, hi = 0, cnt = 0;  // wave-uniform (from ballots)
     for (int64_t w = w0; w < w1; ++w) {
       const int64_t key = 64 * w + lane;
       const bool visible = key < cols && rp[key * sk] != 0;
@@ -155,10 +173,11 @@ __global__ void __launch_bounds__(64 * kPackWaves) fa_pack_mask_kernel(
       if (RANGES && bits != 0) {
         lo = min(lo, (int)(64 * w) + (int)__builtin_ctzll(bits));
         hi = max(hi, (int)(64 * w) + 64 - (int)__builtin_clzll(bits));
+        cnt += __builtin_popcountll(bits);
       }
     }
     if (RANGES && lane == 0) {
-      ranges[2 * row] = hi > 0 ? lo : (int)cols;
+      ranges[2 * row] = range_first(lo, hi, cnt, cols);
       ranges[2 * row + 1] = hi;
     }
   }

@@ -120,13 +120,18 @@ typedef struct fa_fwd_params {
   int64_t mask_keys_stride_b, mask_keys_stride_k;
   /* Optional, with mask_bits: for each mask row, the first visible key and
    * one past the last one (an int32 pair; [seq_len_kv, 0] for a row that
-   * sees no key), as fa_sm75_pack_mask_ranges writes them.  Strides in
-   * pairs, one per mask dimension (0 broadcasts).  The fused kernel then
-   * skips the key tiles outside the span of its rows: a causal mask given as
-   * bits (what transformers builds for a padded prefill, with is_causal
-   * false) costs what the causal flag does, and padding is not computed.
-   * Pairs that claim less than the bits show would hide keys: they must come
-   * from the same mask.  No reference counterpart. */
+   * sees no key), as fa_sm75_pack_mask_ranges writes them; bit 31 of the
+   * first entry set means every key between the two is visible (the row
+   * sees exactly that interval: causal, padding and sliding-window rows).
+   * Strides in pairs, one per mask dimension (0 broadcasts).  The fused
+   * kernel then skips the key tiles outside the span of its rows, and reads
+   * no mask word for a tile inside the interval of every row of a wave whose
+   * rows all carry the bit: a causal mask given as bits (what transformers
+   * builds for a padded prefill, with is_causal false) costs about what the
+   * causal flag does, and padding is not computed.  Pairs that claim less
+   * than the bits show, or the bit for a row with a hidden key inside its
+   * interval, would change the result: they must come from the same mask.
+   * No reference counterpart. */
   const int32_t* mask_ranges;
   int64_t mask_ranges_stride_b, mask_ranges_stride_h, mask_ranges_stride_q;
 } fa_fwd_params;
@@ -178,7 +183,8 @@ int fa_sm75_pack_mask(const uint8_t* mask, int64_t batch, int64_t heads, int64_t
 
 /* fa_sm75_pack_mask that also writes, for each row, the first visible key
  * and one past the last one into ranges ([batch, heads, rows, 2] int32
- * contiguous; [cols, 0] for a row with no visible key), for
+ * contiguous; [cols, 0] for a row with no visible key), bit 31 of the first
+ * set when every key between them is visible, for
  * fa_fwd_params.mask_ranges.  No reference counterpart. */
 int fa_sm75_pack_mask_ranges(const uint8_t* mask, int64_t batch, int64_t heads, int64_t rows,
                              int64_t cols, int64_t stride_b, int64_t stride_h,
@@ -302,7 +308,7 @@ int fa_sm75_backward(const fa_bwd_params* p);
  * or p is NULL). */
 int64_t fa_sm75_backward_workspace_size(const fa_bwd_params* p);
 
-#define FA_SM75_ABI_VERSION 6
+#define FA_SM75_ABI_VERSION 7
 
 /* ---- Reference launcher signatures ------------------------------------ */
 

@@ -265,7 +265,7 @@ def test_mask_ranges_validation(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_sm75_abi_version() == 6
+    assert lib.fa_sm75_abi_version() == 7
 
 
 def test_kernel_policy_switch(lib):

@@ -394,7 +394,8 @@ def _pack_ranges_lib():
 @pytest.mark.parametrize("nk,sk", [(1, 1), (200, 1), (1500, 1), (2500, 1), (300, 3)])
 def test_pack_mask_ranges(device, nk, sk):
     """Each row's first visible key and one past the last ([nk, 0] for a row
-    that sees none) next to the same bits as fa_sm75_pack_mask, for rows of
+    that sees none), bit 31 of the first set exactly when every key between
+    them is visible, next to the same bits as fa_sm75_pack_mask, for rows of
     consecutive bytes and strided ones."""
     lib = _pack_ranges_lib()
     B, H, R = 2, 3, 5
@@ -403,12 +404,12 @@ def test_pack_mask_ranges(device, nk, sk):
     for b in range(B):
         for h in range(H):
             for r in range(R):
-                kind = (b * 15 + h * 5 + r) % 4
+                kind = (b * 15 + h * 5 + r) % 5
                 if kind == 0:  # empty row
                     continue
                 lo = int(torch.randint(0, nk, (1,), generator=g))
                 hi = int(torch.randint(lo + 1, nk + 1, (1,), generator=g)) if kind != 3 else lo + 1
-                row = torch.rand(nk, generator=g) < 0.5
+                row = torch.rand(nk, generator=g) < (1.0 if kind == 4 else 0.5)  # 4: an interval
                 row[:lo] = False
                 row[hi:] = False
                 row[lo] = True
@@ -435,7 +436,10 @@ def test_pack_mask_ranges(device, nk, sk):
             for r in range(R):
                 idx = np.nonzero(mn[b, h, r])[0]
                 exp = (idx[0], idx[-1] + 1) if idx.size else (nk, 0)
-                assert tuple(got[b, h, r]) == exp, (b, h, r, tuple(got[b, h, r]), exp)
+                dense = idx.size > 0 and idx[-1] + 1 - idx[0] == idx.size
+                first = int(got[b, h, r, 0])
+                assert (first & 0x7FFFFFFF, int(got[b, h, r, 1])) == exp, (b, h, r, first, exp)
+                assert (first < 0) == dense, (b, h, r, first, dense)
 
 
 RANGE_CASES = [
