@@ -449,12 +449,26 @@ RANGE_CASES = [
     (2, 4, 4, 300, 900, 64, False, "causal+pad", 0),       # Nq < Nk (chunked prefill with cache)
     (2, 16, 4, 2048, 2048, 128, False, "causal+pad", 3),   # dynamic schedule: several items per WG
     (2, 4, 2, 513, 513, 128, False, "per-head", 0),        # random per-head rows
+    # rows that see exactly an interval (bit 31 of the first entry): a sliding window of its
+    # own width per head, and causal padding with holes punched into a few rows, so some
+    # waves mix interval rows with others and must read their mask words
+    (2, 4, 2, 900, 900, 64, False, "window", 0),
+    (1, 8, 2, 1100, 1100, 128, False, "holes", 0),
+    (2, 4, 4, 700, 700, 128, True, "holes", 3),
 ]
 
 
 def _range_mask(kind, B, Hq, Nq, Nk, g):
     if kind == "per-head":
         return torch.rand(B, Hq, Nq, Nk, generator=g) < 0.3
+    if kind == "window":  # query i sees keys (i - w_h, i], w_h per head
+        i = torch.arange(Nq)[:, None]
+        j = torch.arange(Nk)[None, :]
+        m = torch.zeros(B, Hq, Nq, Nk, dtype=torch.bool)
+        for h in range(Hq):
+            w = [37, 150, 400, Nk][h % 4]
+            m[:, h] = (j <= i) & (j > i - w)
+        return m
     # causal (bottom-right for Nq < Nk) and left padding of B different lengths
     i = torch.arange(Nq)[:, None] + (Nk - Nq)
     j = torch.arange(Nk)[None, :]
@@ -462,6 +476,9 @@ def _range_mask(kind, B, Hq, Nq, Nk, g):
     for b in range(B):
         pad = (b * Nk) // (2 * B)
         m[b, :, :, :pad] = False
+    if kind == "holes":  # a hidden key inside the interval of every 40th row
+        for r in range(5, Nq, 40):
+            m[:, :, r, r // 2] = False
     return m
 
 
