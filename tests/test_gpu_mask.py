@@ -391,7 +391,8 @@ def _pack_ranges_lib():
     return lib
 
 
-@pytest.mark.parametrize("nk,sk", [(1, 1), (200, 1), (1500, 1), (2500, 1), (300, 3)])
+@pytest.mark.parametrize("nk,sk", [(1, 1), (200, 1), (1500, 1), (2500, 1), (4100, 1), (8192, 1),
+                                   (9001, 1), (300, 3)])
 def test_pack_mask_ranges(device, nk, sk):
     """Each row's first visible key and one past the last ([nk, 0] for a row
     that sees none), bit 31 of the first set exactly when every key between
