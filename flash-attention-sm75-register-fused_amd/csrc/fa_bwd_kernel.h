@@ -193,25 +193,26 @@ __global__ void __launch_bounds__(512, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = (float16v)0.0f;
 
-  // Mask ranges (a.mranges): the query rows whose span of visible keys
-  // meets this block's keys [k0, k0 + 128) (over the group's heads when the
-  // mask has a head dimension); the query tiles outside them see no key of
-  // the block, so skipping them changes no result.  Each thread scans a
-  // share of the rows, the wave and then the workgroup (through the P
+  // Mask ranges (a.mranges): the query tiles whose span of visible keys
+  // (the union of their rows' spans, a.tspans, which the dQ kernel wrote)
+  // meets this block's keys [k0, k0 + 128), over the group's heads when the
+  // mask has a head dimension; the other tiles have no row that sees a key
+  // of the block, so skipping them changes no result (a tile kept because
+  // only its union meets the block adds exact zeros).  Each thread scans a
+  // share of the tiles, the wave and then the workgroup (through the P
   // exchange buffers, idle until the first period) take the union.
   int qt_lo = 0, qt_hi = a.qtiles;
   if constexpr (MASK) {
     if (a.mranges != nullptr) {
-      int lo = N, hi = 0;
+      int lo = a.qtiles, hi = 0;
       const int heads = a.mrsh != 0 ? a.group : 1;
-      for (int r = (int)threadIdx.x; r < N; r += 512) {
-        for (int h = 0; h < heads; ++h) {
-          const int32_t* rr = a.mranges + 2 * (b * a.mrsb + (int64_t)(hkv * a.group + h) * a.mrsh +
-                                               (int64_t)r * a.mrsq);
-          if (range_first_key(rr[0]) < k0 + kBwdBlockKeys && rr[1] > k0) {
-            lo = min(lo, r);
-            hi = max(hi, r + 1);
-          }
+      for (int e = (int)threadIdx.x; e < heads * a.qtiles; e += 512) {
+        const int h = e / a.qtiles, qt = e - h * a.qtiles;
+        const int32_t* ts =
+            a.tspans + 2 * ((int64_t)(b * a.hq + hkv * a.group + h) * a.qtiles + qt);
+        if (ts[0] < k0 + kBwdBlockKeys && ts[1] > k0) {
+          lo = min(lo, qt);
+          hi = max(hi, qt + 1);
         }
       }
 #pragma unroll
@@ -233,8 +234,8 @@ __global__ void __launch_bounds__(512, 1) fa_bwd_dkdv_kernel(const BwdArgs a) {
       __syncthreads();  // every wave has read the exchange before it is reused
       lo = __builtin_amdgcn_readfirstlane(lo);
       hi = __builtin_amdgcn_readfirstlane(hi);
-      qt_lo = hi > lo ? lo / kBwdStatsTile : 0;
-      qt_hi = hi > lo ? (hi + kBwdStatsTile - 1) / kBwdStatsTile : 0;
+      qt_lo = hi > lo ? lo : 0;
+      qt_hi = hi > lo ? hi : 0;
     }
   }
   const int qt_begin =
@@ -674,6 +675,17 @@ __global__ void __launch_bounds__(256, MASK && D == 128 ? 1 : 2) fa_bwd_dq_kerne
         xs[2 * wave + 1] = span_hi;
       }
       __syncthreads();
+      // The span of each 64-row query tile of the block (waves 2t and 2t+1)
+      // for the dK/dV kernel, which runs after this one (rows past N carry
+      // row N - 1's pair: a superset, which skips less and changes nothing).
+      if ((wave & 1) == 0 && lane == 0) {
+        const int qt = (q0 + 32 * wave) / kBwdStatsTile;
+        if (qt < a.qtiles) {
+          int32_t* const ts = a.tspans + 2 * ((int64_t)bh * a.qtiles + qt);
+          ts[0] = min(xs[2 * wave], xs[2 * wave + 2]);
+          ts[1] = max(xs[2 * wave + 1], xs[2 * wave + 3]);
+        }
+      }
 #pragma unroll
       for (int w2 = 0; w2 < 4; ++w2) {
         span_lo = min(span_lo, xs[2 * w2]);

@@ -563,6 +563,11 @@ int fa_sm75_backward(const fa_bwd_params* p) {
   a.dksb = p->dk_stride_b; a.dksh = p->dk_stride_h; a.dksn = p->dk_stride_n;
   a.dvsb = p->dv_stride_b; a.dvsh = p->dv_stride_h; a.dvsn = p->dv_stride_n;
   a.stats = static_cast<float*>(p->workspace);
+  a.tspans = p->mask_ranges != nullptr
+                 ? reinterpret_cast<int32_t*>(static_cast<char*>(p->workspace) +
+                                              fa::bwd_stats_bytes(p->batch, p->heads_q,
+                                                                  p->seq_len))
+                 : nullptr;
   a.mbits = p->mask_bits;
   a.msb = p->mask_stride_b;
   a.msh = p->mask_stride_h;

@@ -174,6 +174,11 @@ struct BwdArgs {
   // lse * log2(e) (+inf for rows past N and rows that see no key), then 64
   // floats -rowsum(dO * O) (0 past N); the dQ kernel writes it.
   float* stats;
+  // With mask ranges: after the stats, per (b, query head) and 64-row query
+  // tile, the union [first, one past last) of its rows' spans of visible
+  // keys (an int32 pair), which the dQ kernel writes and the dK/dV kernel
+  // scans in place of every row's pair; nullptr without mask ranges.
+  int32_t* tspans;
   const uint64_t* mbits;   // explicit mask bits (fa_fwd_params layout) or nullptr
   int64_t msb, msh, msq;   // its strides in 64-bit words
   const int32_t* mranges;  // per mask row (first, one past last) visible key, or nullptr
@@ -197,10 +202,16 @@ struct BwdArgs {
 constexpr int kBwdStatsTile = 64;    // query rows per stats record
 constexpr int kBwdBlockKeys = 128;   // keys per dK/dV workgroup
 constexpr int kBwdBlockRows = 128;   // query rows per dQ workgroup
-// Workspace bytes of a backward call.
-inline int64_t bwd_workspace_bytes(int64_t batch, int64_t heads_q, int64_t seq_len) {
+// Workspace bytes of a backward call: the statistics records, then the
+// query tiles' key spans (BwdArgs::stats, tspans).
+inline int64_t bwd_stats_bytes(int64_t batch, int64_t heads_q, int64_t seq_len) {
   return batch * heads_q * ((seq_len + kBwdStatsTile - 1) / kBwdStatsTile) *
          (2 * kBwdStatsTile) * (int64_t)sizeof(float);
+}
+inline int64_t bwd_workspace_bytes(int64_t batch, int64_t heads_q, int64_t seq_len) {
+  return bwd_stats_bytes(batch, heads_q, seq_len) +
+         batch * heads_q * ((seq_len + kBwdStatsTile - 1) / kBwdStatsTile) * 2 *
+             (int64_t)sizeof(int32_t);
 }
 // Launches the dQ and dK/dV kernels; all arguments validated.
 int launch_backward(const BwdArgs& a, int batch, int head_dim, bool causal, bool bf16,

@@ -303,9 +303,10 @@ void fa_sm75_set_contiguous_bwd_strides(fa_bwd_params* p);
  * before touching the device.  Returns FA_OK or an fa_status. */
 int fa_sm75_backward(const fa_bwd_params* p);
 
-/* Workspace bytes fa_sm75_backward needs: 512 per (batch, query head, 64
- * query rows), from batch, heads_q and seq_len alone (0 if one is negative
- * or p is NULL). */
+/* Workspace bytes fa_sm75_backward needs: 520 per (batch, query head, 64
+ * query rows) -- that tile's row statistics, then its span of visible keys
+ * when mask_ranges is given -- from batch, heads_q and seq_len alone (0 if
+ * one is negative or p is NULL). */
 int64_t fa_sm75_backward_workspace_size(const fa_bwd_params* p);
 
 #define FA_SM75_ABI_VERSION 7

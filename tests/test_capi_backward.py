@@ -47,9 +47,9 @@ def test_contiguous_strides(lib):
 
 
 def test_workspace_size(lib):
-    # 512 bytes per (batch, query head, 64 query rows)
-    assert lib.fa_sm75_backward_workspace_size(ctypes.byref(make(lib))) == 2 * 8 * 2 * 512
-    assert lib.fa_sm75_backward_workspace_size(ctypes.byref(make(lib, seq_len=64))) == 2 * 8 * 512
+    # 520 bytes per (batch, query head, 64 query rows): the stats record, then the tile's key span
+    assert lib.fa_sm75_backward_workspace_size(ctypes.byref(make(lib))) == 2 * 8 * 2 * 520
+    assert lib.fa_sm75_backward_workspace_size(ctypes.byref(make(lib, seq_len=64))) == 2 * 8 * 520
     assert lib.fa_sm75_backward_workspace_size(ctypes.byref(make(lib, seq_len=0))) == 0
     assert lib.fa_sm75_backward_workspace_size(None) == 0
 

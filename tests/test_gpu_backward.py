@@ -385,20 +385,35 @@ def per_head_mask(B, Hq, N, seed):
     return m
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,N,D,bf16,per_head",
-                         [(3, 4, 2, 700, 64, False, False), (2, 8, 2, 1100, 128, True, False),
-                          (2, 8, 2, 600, 64, False, True), (1, 6, 2, 900, 128, False, True)])
-def test_backward_mask_ranges_bitwise(device, B, Hq, Hkv, N, D, bf16, per_head):
+def split_mask(B, N):
+    """[B, 1, N, N] mask whose rows alternate between two disjoint key spans:
+    even rows see the first 96 keys, odd rows the last 96.  Every 64-row query
+    tile's span (the union over its rows) then covers all keys although no
+    row sees a key in between, so the dK/dV kernel keeps query tiles that
+    contribute nothing to its key blocks there."""
+    i = torch.arange(N)
+    even = (i[:, None] % 2 == 0) & (i[None, :] < 96)
+    odd = (i[:, None] % 2 == 1) & (i[None, :] >= N - 96)
+    return (even | odd)[None, None].expand(B, 1, N, N).clone()
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,bf16,kind",
+                         [(3, 4, 2, 700, 64, False, "padded"), (2, 8, 2, 1100, 128, True, "padded"),
+                          (2, 8, 2, 600, 64, False, "per_head"), (1, 6, 2, 900, 128, False, "per_head"),
+                          (2, 4, 2, 640, 64, False, "split"), (1, 4, 1, 520, 128, True, "split")])
+def test_backward_mask_ranges_bitwise(device, B, Hq, Hkv, N, D, bf16, kind):
     """Through the C ABI: a mask given as bits, with and without mask_ranges:
     dQ, dK and dV bit for bit the same (the skipped key tiles of dQ and query
     tiles of dK/dV see nothing of each other), and within the bar of the
     float64 closed form.  The mask is a causal one with left padding shared
-    by every head, or (per_head) a [B, Hq, N, N] mask whose rows' spans differ
-    between the query heads of a group and some of whose rows see no key."""
+    by every head ("padded"), a [B, Hq, N, N] mask whose rows' spans differ
+    between the query heads of a group and some of whose rows see no key
+    ("per_head"), or rows alternating between two disjoint key spans
+    ("split", split_mask)."""
+    per_head = kind == "per_head"
     import ctypes
     from capi_types import LIB, BwdParams
-    print(f"[bwd ranges] B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} bf16={bf16} per_head={per_head}",
-          flush=True)
+    print(f"[bwd ranges] B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} bf16={bf16} kind={kind}", flush=True)
     lib = ctypes.CDLL(LIB)
     lib.fa_sm75_backward.argtypes = [ctypes.POINTER(BwdParams)]
     lib.fa_sm75_backward_workspace_size.argtypes = [ctypes.POINTER(BwdParams)]
@@ -412,6 +427,8 @@ def test_backward_mask_ranges_bitwise(device, B, Hq, Hkv, N, D, bf16, per_head):
     q, k, v, do = (torch.randn(B, h, N, D, generator=g).to(dt) for h in (Hq, Hkv, Hkv, Hq))
     if per_head:
         m = per_head_mask(B, Hq, N, N + D)
+    elif kind == "split":
+        m = split_mask(B, N)
     else:
         i = torch.arange(N)
         m = (i[None, :] <= i[:, None])[None, None].expand(B, 1, N, N).clone()
