@@ -109,7 +109,12 @@ template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, int MASK_MODE, boo
 __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
   constexpr bool MASK = MASK_MODE != 0;        // an explicit mask: bits or key bytes
   constexpr bool KEY_BYTES = MASK_MODE == 2;   // key-padding bytes (a.mkeys)
-  using L = Lds<D>;
+  // LDS tile layout: dense (no row padding, 8 direct loads per tile instead
+  // of 12; interleaved A/B on head_dim-64 launches 1.013-1.031x, results
+  // bitwise unchanged) for the 4-wave head_dim-64 kernel, padded otherwise
+  // (the key split's exchange areas need the padded tile's size).
+  constexpr bool DENSE = D == 64 && WAVES == 4 && !KSPLIT;
+  using L = std::conditional_t<DENSE, LdsDense<D>, Lds<D>>;
   using E = Elem<BF16>;
   constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
   constexpr int MT = D / 32;       // 32-row output tiles of O^T
@@ -408,7 +413,11 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       const int pos = (wq + 4 * s) * 1024 + 16 * lane;  // bytes into the tile
       const int row = pos / (2 * L::Pitch);
       const int within = pos - row * (2 * L::Pitch);
-      if (within < 2 * D) {
+      if constexpr (DENSE) {  // 8 rows of 128 bytes per segment, no padding
+        const int c = (within >> 4) ^ dense_swizzle(row);
+        goff_a[s] = (int)(row * a_stride * 2) + 16 * c;
+        if (OWN_B) goff_b[s] = (int)(row * a.vsn * 2) + 16 * c;
+      } else if (within < 2 * D) {
         const int c = (within >> 4) ^ ((row >> 2) & 3);
         goff_a[s] = (int)(row * a_stride * 2) + 16 * c;
         if (OWN_B) goff_b[s] = (int)(row * a.vsn * 2) + 16 * c;
@@ -463,8 +472,12 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
         direct_load16(r, lds_seg(dst, s), (is_v && OWN_B) ? goff_b[s] : goff_a[s]);
     };
 
-    // Per-lane LDS bases of the operand reads (see Lds): K rows ql (+32t),
-    // chunk 2kk + hi; V rows 16ks + 4hi + gi/4 (+8), dims 32mt + 16(grp&1) + 4(gi&3).
+    // Per-lane LDS bases of the operand reads (see Lds, LdsDense): K rows ql
+    // (+32t), chunk 2kk + hi; V rows 16ks + 4hi + gi/4 (+8), dims 32mt +
+    // 16(grp&1) + 4(gi&3).  Padded: the swizzle touches the low two chunk bits,
+    // so two K bases (kk even, odd) and two V bases (rows +0, +8) with
+    // immediates for the rest; dense: one K base per kk and two V bases per
+    // 64-dim half (mt).
     const int sK = (ql >> 2) & 3;
     const int k_base_even = ql * L::Pitch + 8 * (hi ^ sK);
     const int k_base_odd = ql * L::Pitch + 8 * ((2 + hi) ^ sK);
@@ -472,10 +485,23 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     const int v_c = 2 * (grp & 1) + ((gi & 3) >> 1);
     const int v_base0 = v_row * L::Pitch + 8 * (v_c ^ hi) + 4 * (gi & 1);
     const int v_base1 = (v_row + 8) * L::Pitch + 8 * (v_c ^ (hi + 2)) + 4 * (gi & 1);
+    int kd_base[DENSE ? KK : 1], vd_base0[DENSE ? MT : 1], vd_base1[DENSE ? MT : 1];
+    if constexpr (DENSE) {
+      const int sw = dense_swizzle(ql);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) kd_base[kk] = ql * L::Pitch + 8 * ((2 * kk + hi) ^ sw);
+      const int sw0 = dense_swizzle(v_row), sw1 = dense_swizzle(v_row + 8);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        vd_base0[mt] = v_row * L::Pitch + 8 * ((v_c + 4 * mt) ^ sw0) + 4 * (gi & 1);
+        vd_base1[mt] = (v_row + 8) * L::Pitch + 8 * ((v_c + 4 * mt) ^ sw1) + 4 * (gi & 1);
+      }
+    }
 
     // K operand i (sub-tile t = i / KK, step kk = i % KK) of one K buffer.
     auto read_k = [&](const _Float16* Ks, int i) -> half8 {
       const int t = i / KK, kk = i % KK;
+      if constexpr (DENSE) return *(const half8*)(Ks + kd_base[kk] + 32 * t * L::Pitch);
       const int off = ((kk & 1) ? k_base_odd : k_base_even) + 32 * t * L::Pitch + 32 * (kk >> 1);
       return *(const half8*)(Ks + off);
     };
@@ -490,6 +516,12 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     auto read_v = [&](const _Float16* Vs, int v) -> half8 {
       const int ks = v / MTX, mt = v % MTX;
       if (ROWSUM && mt == MT) return ones_a;
+      if constexpr (DENSE) {
+        const int imm = 16 * ks * L::Pitch;
+        const half4 lo = ds_read_tr16(Vs + vd_base0[mt] + imm);
+        const half4 hi4 = ds_read_tr16(Vs + vd_base1[mt] + imm);
+        return __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
       const int imm = 16 * ks * L::Pitch + 32 * mt;
       const half4 lo = ds_read_tr16(Vs + v_base0 + imm);
       const half4 hi4 = ds_read_tr16(Vs + v_base1 + imm);

@@ -124,6 +124,32 @@ struct Lds {
   static_assert(Segs % 4 == 0, "segments must split over 4 waves");
 };
 
+// Dense LDS tile layout (the 4-wave forward kernel at head_dim 64): rows of
+// D halves with no padding, so a 64-key tile is 8 KB and arrives in 8 direct
+// loads of 1 KB where the padded one takes 12.  Chunk c of row r is stored
+// at chunk c ^ dense_swizzle(r), a 3-bit value of (r >> 1) & 7 whose bits are
+// reordered so that rows r and r + 2 differ in bit 2:
+//  * K operand ds_read_b128 (16 lanes = 16 consecutive rows, one chunk): the
+//    8 even rows take 8 distinct chunks of the first 128 bytes of the bank
+//    sweep, the 8 odd rows 8 distinct chunks of the second;
+//  * transposing V reads (32 lanes = rows 4k..4k+3, the same 64 bytes of
+//    each): rows 4k and 4k+2 (likewise 4k+1 and 4k+3) land in opposite
+//    64-byte halves of their 128 bytes.
+// dense_swizzle(r + 16) = dense_swizzle(r), so the rows of one operand read
+// 16 or 32 apart share a per-lane base; chunk bit 2 is swizzled, so each
+// 64-dim half of a row (chunks 0-3 or 4-7) takes a base of its own.
+template <int D>
+struct LdsDense {
+  static_assert(D == 64, "dense layout: head_dim 64");
+  static constexpr int Pitch = D;               // halves per row
+  static constexpr int Tile = kBlockN * Pitch;  // halves per K (or V) tile
+  static constexpr int Segs = Tile * 2 / 1024;  // 1 KB direct-load segments
+};
+__device__ __forceinline__ int dense_swizzle(int r) {
+  const int m = (r >> 1) & 7;
+  return ((m & 1) << 2) | (m >> 1);
+}
+
 __device__ __forceinline__ half4 ds_read_tr16(const _Float16* p) {
   short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) short4v*)(p));
