@@ -90,10 +90,12 @@ namespace {
 // tail (measured: C3 +3.4%, B=1 Hq=14 Hkv=2 N=4096 +4.8%; launches that keep
 // two waves per SIMD busy throughout lose 1-2%, the extra matrix work costing
 // clock).
-// LDS through which group 1 of a paired key split hands its share of block A
-// to group 0: per row wave, MT * 1024 floats of O (four consecutive floats of
-// a lane's accumulator per 16-byte slot), then 64 running maxima and 64 lane
-// partial sums.  Only the instances that run pairs allocate it.
+// LDS through which group 1 of a key split hands its share of a block to
+// group 0: per row wave, MT * 1024 floats of O (four consecutive floats of a
+// lane's accumulator per 16-byte slot), then 64 running maxima and 64 lane
+// partial sums.  Allocated by the head_dim-64 key-split instances, whose
+// dense tiles are smaller than that (the head_dim-128 ones hand over through
+// a padded tile array, which the main loop no longer reads).
 template <bool P, int MT>
 __device__ __forceinline__ float* pair_exchange() {
   if constexpr (P) {
@@ -111,9 +113,9 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   constexpr bool KEY_BYTES = MASK_MODE == 2;   // key-padding bytes (a.mkeys)
   // LDS tile layout: dense (no row padding, 8 direct loads per tile instead
   // of 12; interleaved A/B on head_dim-64 launches 1.013-1.031x, results
-  // bitwise unchanged) for the 4-wave head_dim-64 kernel, padded otherwise
-  // (the key split's exchange areas need the padded tile's size).
-  constexpr bool DENSE = D == 64 && WAVES == 4 && !KSPLIT;
+  // bitwise unchanged) at head_dim 64, padded at head_dim 128 (whose dense
+  // swizzle would take more per-lane bases than its registers hold).
+  constexpr bool DENSE = D == 64;
   using L = std::conditional_t<DENSE, LdsDense<D>, Lds<D>>;
   using E = Elem<BF16>;
   constexpr int KK = D / 16;       // 16-wide contraction steps of S^T
@@ -557,7 +559,8 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // Pair mode, group 1: its share of block A (unnormalised O, running max,
     // lane partial sums) into the exchange area for group 0, and a fresh
     // state for block B.
-    float* const pair_xo = pair_exchange<PAIRS, MT>() + (PAIRS ? rw * (MT * 1024 + 128) : 0);
+    constexpr bool XAREA = KSPLIT && D == 64;  // the exchange area (pair_exchange)
+    float* const pair_xo = pair_exchange<XAREA, MT>() + (XAREA ? rw * (MT * 1024 + 128) : 0);
     auto hand_off_a = [&]() {
       if constexpr (PAIRS) {
 #pragma unroll
@@ -861,13 +864,13 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     if constexpr (KSPLIT) {
       // Group 1 wave w+4 hands its O (unnormalised), running max and partial
       // sums to group 0 wave w (same rows, same lane layout) through the
-      // group-1 half of one LDS array, which no wave reads any more (pair
-      // mode: the exchange area, which a group 1 that moved on to block B
-      // filled already).
+      // exchange area (head_dim 64; in pair mode a group 1 that moved on to
+      // block B filled it already) or the group-1 half of one LDS array,
+      // which no wave reads any more (head_dim 128).
       __syncthreads();
       _Float16* const arr = rw == 0 ? k_lds0 : rw == 1 ? k_lds1 : rw == 2 ? v_lds0 : v_lds1;
-      float* const xo = pairs ? pair_xo : (float*)(arr + L::Tile);
-      static_assert(MT * 16 * 64 * 4 + 2 * 64 * 4 <= L::Tile * 2, "exchange fits a tile");
+      float* const xo = XAREA ? pair_xo : (float*)(arr + L::Tile);
+      static_assert(XAREA || MT * 16 * 64 * 4 + 2 * 64 * 4 <= L::Tile * 2, "exchange fits a tile");
       if (kgrp == 1 && !g1b) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
