@@ -56,12 +56,27 @@ constexpr int kDecTargetWgs = 256; // one workgroup per CU (measured best)
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
+// Per-wave V tile: 32 rows of D halves with no padding (a direct load costs
+// its wave about the same per instruction whatever it moves, so padding
+// lanes were a third of the loads at head_dim 64, a fifth at 128).  Only the
+// transposing V reads touch this tile, and each reads the same 64 bytes of
+// rows 4k..4k+3 (and 4k+8..): chunk c of row r is stored at c ^ swz(r) so
+// that those four rows land in four disjoint 64-byte windows of the 256-byte
+// bank sweep -- at head_dim 64 (128-byte rows) rows 4k and 4k+2 differ in
+// chunk bit 2 (dense_swizzle, as the prefill kernel's dense tiles), at 128
+// (256-byte rows, one sweep each) chunk bits 2-3 take the row's position in
+// its group of four.  swz(r + 16) = swz(r), so the two 16-key halves share a
+// base; the XOR reaches chunk bit 2, so each 32-dim output tile has its own.
 template <int D>
 struct DecLds {
-  static constexpr int Pitch = D + 32;                 // same padded rows as Lds<D>
+  static constexpr int Pitch = D;                      // halves per row
   static constexpr int Tile = kDecTile * Pitch;        // halves per V tile
   static constexpr int Segs = Tile * 2 / 1024;         // 1 KB direct-load segments
   static_assert(Tile * 2 % 1024 == 0, "V tile must be whole segments");
+  static __device__ __forceinline__ int swz(int r) {
+    if constexpr (D == 64) return dense_swizzle(r);
+    else return (r & 3) << 2;
+  }
 };
 
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
@@ -95,6 +110,10 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   // Per-wave V tiles: wave w uses [w * Tile, (w + 1) * Tile) of each array.
   __shared__ __attribute__((aligned(1024))) _Float16 v_lds0[kWaves * L::Tile];
   __shared__ __attribute__((aligned(1024))) _Float16 v_lds1[kWaves * L::Tile];
+  // Each wave's running max and row sums for the final merge (its O goes to
+  // its two V tiles, which it fills exactly: MT 32 x 32 float tiles).
+  __shared__ float ml_lds[kWaves * 128];
+  static_assert(MT / 2 * 16 * 64 * 4 <= L::Tile * 2, "O of a wave fits its V tiles");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -182,12 +201,8 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     const int pos = s * 1024 + 16 * lane;
     const int row = pos / (2 * L::Pitch);
     const int within = pos - row * (2 * L::Pitch);
-    if (within < 2 * D) {
-      const int c = (within >> 4) ^ ((row >> 2) & 3);
-      goff_v[s] = (int)(row * a.vsn * 2) + 16 * c;
-    } else {
-      goff_v[s] = -16;  // padding: past any window -> zeros
-    }
+    const int c = (within >> 4) ^ L::swz(row);
+    goff_v[s] = (int)(row * a.vsn * 2) + 16 * c;
   }
   auto load_v = [&](int it, _Float16* tile, bool valid) {
     const int kb = key0 + (wave + kWaves * it) * kDecTile;
@@ -232,15 +247,21 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     return __builtin_amdgcn_raw_buffer_load_b32(rmask, m_voff + 4 * tile, 0, 0);
   };
 
+  // Per-lane bases of the transposing V reads: rows 16ks + 4hi + gi/4
+  // (+8), dims 32mt + 16(grp&1) + 4(gi&3), one pair of bases per mt.
   const int v_row = 4 * hi + (gi >> 2);
   const int v_c = 2 * (grp & 1) + ((gi & 3) >> 1);
-  const int v_base0 = v_row * L::Pitch + 8 * (v_c ^ hi) + 4 * (gi & 1);
-  const int v_base1 = (v_row + 8) * L::Pitch + 8 * (v_c ^ (hi + 2)) + 4 * (gi & 1);
+  int v_base0[MT], v_base1[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    v_base0[mt] = v_row * L::Pitch + 8 * ((v_c + 4 * mt) ^ L::swz(v_row)) + 4 * (gi & 1);
+    v_base1[mt] = (v_row + 8) * L::Pitch + 8 * ((v_c + 4 * mt) ^ L::swz(v_row + 8)) + 4 * (gi & 1);
+  }
   auto read_v = [&](const _Float16* Vs, int v) -> half8 {
     const int ks = v / MT, mt = v % MT;
-    const int imm = 16 * ks * L::Pitch + 32 * mt;
-    const half4 lo = ds_read_tr16(Vs + v_base0 + imm);
-    const half4 hi4 = ds_read_tr16(Vs + v_base1 + imm);
+    const int imm = 16 * ks * L::Pitch;
+    const half4 lo = ds_read_tr16(Vs + v_base0[mt] + imm);
+    const half4 hi4 = ds_read_tr16(Vs + v_base1[mt] + imm);
     return __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
@@ -383,7 +404,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
 #pragma unroll
       for (int i = 0; i < 16; ++i) dst[i * 64 + lane] = oacc[mt][i];
     }
-    float* ml = o_lo + (MT / 2) * 16 * 64;
+    float* ml = ml_lds + wave * 128;
     ml[lane] = m_run;
     ml[64 + lane] = l_tot;
   }
@@ -393,7 +414,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
   float m_w[kWaves], M = -__builtin_inff();
 #pragma unroll
   for (int u = 0; u < kWaves; ++u) {
-    const float* ml = (const float*)(v_lds0 + u * L::Tile) + (MT / 2) * 16 * 64;
+    const float* ml = ml_lds + u * 128;
     m_w[u] = ml[lane];
     M = fmaxf(M, m_w[u]);
   }
@@ -406,7 +427,7 @@ __global__ void __launch_bounds__(kThreads, 2) fa_decode_kernel(const DecArgs d)
     const float f = (m_w[u] == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((m_w[u] - M) * c2);
     const float* base = (const float*)((mt < MT / 2 ? v_lds0 : v_lds1) + u * L::Tile) +
                         (mt % (MT / 2)) * 16 * 64;
-    const float* ml = (const float*)(v_lds0 + u * L::Tile) + (MT / 2) * 16 * 64;
+    const float* ml = ml_lds + u * 128;
     Ltot += f * ml[64 + lane];
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[i] += f * base[i * 64 + lane];
