@@ -27,12 +27,10 @@ void launch_shape(const FwdArgs& a, int batch, int head_dim, bool causal, Schedu
     launch_fused<64, WAVES, MASK, KSPLIT, BF16>(a, batch, causal, schedule, stream);
 }
 
-// The 8-wave (256-row, one workgroup per CU) kernel only runs when asked
-// for (FA_POLICY_WIDE): measured on C4 it is ~4% slower than the 4-wave
-// kernel -- with one workgroup per CU both waves of a SIMD stop at the same
-// barrier, where two independent 4-wave workgroups cover each other's.  It
-// is built for binary16 only (bfloat16 calls take the 4-wave kernel).
-// Masked calls always take the 4-wave kernel.
+// The 8-wave (256-row, one workgroup per CU) kernel runs when asked for
+// (FA_POLICY_WIDE) and where AUTO picks it (use_wide_workgroups).  It is built
+// for binary16 only (bfloat16 calls take the 4-wave kernel); masked calls
+// always take the 4-wave kernel.
 template <bool BF16>
 void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int policy,
                   hipStream_t stream) {
@@ -46,7 +44,7 @@ void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int po
     return;
   }
   if constexpr (!BF16) {
-    if (policy == 2) {
+    if (policy == 2 || use_wide_workgroups(a, batch, head_dim, causal, policy)) {
       launch_shape<8, 0, false, false>(a, batch, head_dim, causal, Schedule::kStatic, stream);
       return;
     }
@@ -162,6 +160,37 @@ bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int p
   if (use_pair_split(a, batch, head_dim, causal, policy)) return true;
   return causal && head_dim == 128 && planned.num_qblocks >= kSplitMinBlocks &&
          planned.items <= kSplitMaxItems * resident_fused_workgroups();
+}
+
+// AUTO takes the 256-row workgroups of 8 waves (one per CU, K/V triple
+// buffered: every K/V tile serves 256 query rows, so each wave issues half
+// the direct loads per step of the 4-wave kernel, which at ~30 cycles of its
+// wave apiece are a tenth or more of a step) for binary16 launches without a
+// mask that neither key split takes and the dynamic schedule would not run:
+//  * non-causal launches of at most two 128-row blocks per CU, where the
+//    4-wave kernel leaves some CUs with two workgroups and others with one,
+//    and the 8-wave grid gives each CU at most one (interleaved A/B on
+//    MI355X: C2 1.084x, B=3 H=16 N=1024 1.087x at head_dim 64 and 1.060x at
+//    128, B=2 H=24 N=1024 1.104x; B=4 H=12 N=1536, past two, 0.836x);
+//  * rows of at least kWideMinRows queries and keys, non-causal or at
+//    head_dim 64 (1.01-1.07x over 13 shapes, the worst 0.989x, B=2 Hq=32
+//    Hkv=8 N=4096 d64 causal), or causal head_dim 128 from twice that (C4
+//    1.010x, B=2 Hq=32 Hkv=8 N=8192 1.000x; at N=4096 0.971-1.004x).
+// Shorter rows stay on the 4-wave kernel: its causal large/small pairing
+// evens single-round launches out (C3 0.825x on 256-row workgroups), and the
+// 256-row blocks' diagonal costs more of a short row (B=4 Hq=32 Hkv=8 N=2048
+// d128 causal 0.916x, full 0.956x).
+constexpr int kWideMinRows = 4096;
+
+bool use_wide_workgroups(const FwdArgs& a, int batch, int head_dim, bool causal, int policy) {
+  if (policy != 0 || a.bf16 || has_mask(a)) return false;
+  if (use_key_split(a, batch, head_dim, causal, policy)) return false;
+  FwdArgs planned = a;
+  plan_grid(planned, batch, 128);
+  if (use_dynamic_schedule(planned, batch, causal, Schedule::kAuto)) return false;
+  if (!causal && planned.items <= 2 * compute_units()) return true;
+  const int rows = std::min(a.n, a.nk);
+  return rows >= kWideMinRows && (head_dim == 64 || !causal || rows >= 2 * kWideMinRows);
 }
 
 bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedule schedule) {

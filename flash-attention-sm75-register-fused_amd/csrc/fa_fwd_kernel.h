@@ -271,6 +271,8 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     const int q0 = qb * BLOCK_M;
     const int qw = q0 + rw * 32;
     const int qrow = qw + ql;
+    // Causal: the last key tile any row of this wave sees (floor division).
+    const int wave_last_tile = (qw + 31 + a.diag) >> 6;
     const int qw_b = qb_b * BLOCK_M + rw * 32;  // (pairs with a block B)
     const int qrow_b = qw_b + ql;
     const bool g1b = pairs && kgrp == 1 && qb_b >= 0;  // this group moves on to B
@@ -834,7 +836,19 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;
       int j = tile0;
-      for (; j + STAGES < tile_end; j += STAGES) {  // every step has a next tile
+      // Causal, head_dim 64: the wave computes the tiles up to the last one
+      // its rows see (at least the first); the tiles after it lie wholly past
+      // its diagonal, where its scores, probabilities and P V products are
+      // exactly zero, so for those it only issues its share of the loads and
+      // meets the barriers, leaving its SIMD to the waves that still see keys
+      // (the upper waves of a block skip the last tiles of its diagonal; C3
+      // 1.016x, B=1 Hq=32 N=4096 on 256-row workgroups 1.019x, results
+      // bitwise unchanged).  Not at head_dim 128: the extra tail code costs
+      // the 4-wave kernel registers it does not have (spills, 0.90-0.96x),
+      // and the 256-row kernel measured no gain.
+      constexpr bool TRIM = CAUSAL && !KSPLIT && D == 64;
+      const int cend = TRIM ? min(tile_end, max(tile0 + 1, wave_last_tile + 1)) : tile_end;
+      for (; j + STAGES < cend; j += STAGES) {  // every step has a next tile
         step(j, Flag<true>{}, I0{});
         step(j + 1, Flag<true>{}, I1{});
         if constexpr (STAGES == 3) {
@@ -843,16 +857,55 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
           s_buf[0][1] = s_buf[1][1];
         }
       }
-      const int rest = tile_end - j;  // 1 .. STAGES steps left, the last one without a next tile
-      if (rest == 1) {
-        step(j, Flag<false>{}, I0{});
-      } else if (STAGES == 2 || rest == 2) {
-        step(j, Flag<true>{}, I0{});
-        step(j + 1, Flag<false>{}, I1{});
-      } else if constexpr (STAGES == 3) {
-        step(j, Flag<true>{}, I0{});
-        step(j + 1, Flag<true>{}, I1{});
-        step(j + 2, Flag<false>{}, I2{});
+      bool trimmed = false;
+      if constexpr (TRIM) {
+        if (cend < tile_end) {
+          trimmed = true;
+          // 1 .. STAGES computed steps left, each with a next tile (its loads)
+          const int rest = cend - j;
+          step(j, Flag<true>{}, I0{});
+          if (rest >= 2) step(j + 1, Flag<true>{}, I1{});
+          if constexpr (STAGES == 3) {
+            if (rest == 3) step(j + 2, Flag<true>{}, I2{});
+          }
+          for (j += rest; j + 1 < tile_end; ++j) {
+            // Loads of the step at position (j - tile0) % STAGES: K_{j+STAGES}
+            // into K_j's buffer, V_{j+STAGES-1} into V_{j-1}'s.
+            const int u = (j - tile0) % STAGES;
+            _Float16* const k_dst =
+                u == 0 ? kbuf(I0{}) : (u == 1 || STAGES == 2) ? kbuf(I1{}) : kbuf(I2{});
+            const int uv = (u + STAGES - 1) % STAGES;
+            _Float16* const v_dst =
+                uv == 0 ? vbuf(I0{}) : (uv == 1 || STAGES == 2) ? vbuf(I1{}) : vbuf(I2{});
+            const __amdgpu_buffer_rsrc_t rk = k_window(j + STAGES);
+            const __amdgpu_buffer_rsrc_t rv = v_window(j + STAGES - 1);
+            static_for<LPW>([&](auto q_c) {
+              constexpr int q = decltype(q_c)::value;
+              if constexpr (SPLIT_ROLES)
+                direct_load16(v_role ? rv : rk, lds_seg(v_role ? v_dst : k_dst, q), goff_a[q]);
+              else if constexpr (q < SEGQ)
+                direct_load16(rk, lds_seg(k_dst, q), goff_a[q]);
+              else
+                direct_load16(rv, lds_seg(v_dst, q - SEGQ), goff_b[q - SEGQ]);
+            });
+            barrier_after_loads<STAGES == 3 ? LPW : 0>();
+          }
+          // The item's last step: the head claim for the next item.
+          if (prefetch && tid == 0) next_claim = claim(own_q, false);
+        }
+      }
+      if (!trimmed) {
+        const int rest = tile_end - j;  // 1 .. STAGES steps left, the last one without a next tile
+        if (rest == 1) {
+          step(j, Flag<false>{}, I0{});
+        } else if (STAGES == 2 || rest == 2) {
+          step(j, Flag<true>{}, I0{});
+          step(j + 1, Flag<false>{}, I1{});
+        } else if constexpr (STAGES == 3) {
+          step(j, Flag<true>{}, I0{});
+          step(j + 1, Flag<true>{}, I1{});
+          step(j + 2, Flag<false>{}, I2{});
+        }
       }
     }
     // No direct load may land in LDS after the workgroup ends.
