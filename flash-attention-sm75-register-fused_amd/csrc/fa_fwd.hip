@@ -162,10 +162,10 @@ bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int p
          planned.items <= kSplitMaxItems * resident_fused_workgroups();
 }
 
-// AUTO takes the 256-row workgroups of 8 waves (one per CU, K/V triple
-// buffered: every K/V tile serves 256 query rows, so each wave issues half
-// the direct loads per step of the 4-wave kernel, which at ~30 cycles of its
-// wave apiece are a tenth or more of a step) for binary16 launches without a
+// AUTO takes the 256-row workgroups of 8 waves (one per CU: every K/V tile
+// serves 256 query rows, so each wave issues half the direct loads per step
+// of the 4-wave kernel, which at ~30 cycles of its wave apiece are a tenth or
+// more of a step) for binary16 launches without a
 // mask that neither key split takes and the dynamic schedule would not run:
 //  * non-causal launches of at most two 128-row blocks per CU, where the
 //    4-wave kernel leaves some CUs with two workgroups and others with one,

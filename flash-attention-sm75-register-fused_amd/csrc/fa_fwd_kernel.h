@@ -67,10 +67,16 @@ namespace {
 //   * 4 waves, 128 query rows, two workgroups per CU, K/V tiles double
 //     buffered (STAGES = 2): step j loads K_{j+2} and V_{j+1} into the
 //     buffers step j-1 freed, and they must land by the end of step j;
-//   * 8 waves, 256 query rows, one workgroup per CU, triple buffered
-//     (STAGES = 3): step j loads K_{j+3} and V_{j+2}, which have until the
-//     end of step j+1 to land; every K/V tile serves 256 query rows, and each
-//     wave issues half as many direct loads (waves 0-3 load K, 4-7 load V);
+//   * 8 waves, 256 query rows, one workgroup per CU: every K/V tile serves
+//     256 query rows, and each wave issues half as many direct loads (waves
+//     0-3 load K, 4-7 load V).  At head_dim 64 triple buffered (STAGES = 3):
+//     step j loads K_{j+3} and V_{j+2}, which have until the end of step j+1
+//     to land.  At head_dim 128 double buffered like the 4-wave kernel: the
+//     third stage's code (its unrolled rest steps) needs more than the 256
+//     VGPRs of two waves per SIMD and spilled 101 of them, whose scratch
+//     (about 39 MB for the resident waves) goes out to HBM; double buffered
+//     it spills none and runs 1.004-1.018x faster (C4 1.018x, B=2 Hq=32
+//     Hkv=8 N=8192 causal 1.018x, B=1 Hq=32 Hkv=8 N=4096 full 1.004x);
 //   * KSPLIT: 8 waves, 128 query rows, one workgroup per CU: waves w and w+4
 //     own the same 32 rows, and each group of 4 waves runs the 4-wave
 //     pipeline over its half of the block's key tiles in its own half of the
@@ -127,7 +133,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   constexpr int PFV = 2;           // V operand reads run this many MFMAs ahead
   constexpr int ROW_WAVES = KSPLIT ? 4 : WAVES;  // waves owning distinct rows
   constexpr int BLOCK_M = 32 * ROW_WAVES;
-  constexpr int STAGES = WAVES == 8 && !KSPLIT ? 3 : 2;  // K/V buffers per tile kind
+  constexpr int STAGES = WAVES == 8 && !KSPLIT && D == 64 ? 3 : 2;  // K/V buffers per tile kind
   constexpr int SEGQ = L::Segs / 4;               // segments of one tile per wave quarter
   constexpr int LPW = 2 * L::Segs / ROW_WAVES;    // direct loads per wave per step
   constexpr bool SPLIT_ROLES = WAVES == 8 && !KSPLIT;  // a wave loads K or V, not both

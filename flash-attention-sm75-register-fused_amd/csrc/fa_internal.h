@@ -62,7 +62,8 @@ void launch_clear_tickets(uint64_t* ctr, hipStream_t stream);
 // Launches the fused MFMA kernel; all arguments already validated.
 // policy (fa_kernel_policy): 0 = automatic, 1 = 128-row workgroups of 4
 // waves (two per CU) on the static schedule, 2 = 256-row workgroups of 8
-// waves (one per CU, K/V triple-buffered), 3 = 128-row workgroups on the
+// waves (one per CU; K/V triple-buffered at head_dim 64, double at 128),
+// 3 = 128-row workgroups on the
 // dynamic schedule (when a.ctr is set), 4 = 128-row workgroups of 8 waves
 // splitting the keys (one per CU).
 int launch_fused_forward(const FwdArgs& a, int batch, int head_dim, bool causal,

@@ -221,7 +221,8 @@ int fa_sm75_abi_version(void);
  * XCD-balanced schedule for long launches when p->workspace holds its
  * counters.  NARROW forces 128-row workgroups of 4 waves (two per CU) on
  * the static schedule (one workgroup per query block); WIDE forces 256-row
- * workgroups of 8 waves (one per CU, K/V tiles triple-buffered); DYNAMIC
+ * workgroups of 8 waves (one per CU; K/V tiles triple-buffered at
+ * head_dim 64, double-buffered at 128); DYNAMIC
  * forces 128-row workgroups on the dynamic schedule whenever the workspace
  * holds its counters; SPLIT forces 128-row workgroups of 8 waves, two
  * groups of 4 each taking half of the block's key tiles (one per CU);
