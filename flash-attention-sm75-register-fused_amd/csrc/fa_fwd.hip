@@ -28,8 +28,7 @@ void launch_shape(const FwdArgs& a, int batch, int head_dim, bool causal, Schedu
 }
 
 // The 8-wave (256-row, one workgroup per CU) kernel runs when asked for
-// (FA_POLICY_WIDE) and where AUTO picks it (use_wide_workgroups).  It is built
-// for binary16 only (bfloat16 calls take the 4-wave kernel); masked calls
+// (FA_POLICY_WIDE) and where AUTO picks it (use_wide_workgroups); masked calls
 // always take the 4-wave kernel.
 template <bool BF16>
 void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int policy,
@@ -43,11 +42,9 @@ void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int po
     launch_shape<4, 1, false, BF16>(a, batch, head_dim, causal, schedule, stream);
     return;
   }
-  if constexpr (!BF16) {
-    if (policy == 2 || use_wide_workgroups(a, batch, head_dim, causal, policy)) {
-      launch_shape<8, 0, false, false>(a, batch, head_dim, causal, Schedule::kStatic, stream);
-      return;
-    }
+  if (policy == 2 || use_wide_workgroups(a, batch, head_dim, causal, policy)) {
+    launch_shape<8, 0, false, BF16>(a, batch, head_dim, causal, Schedule::kStatic, stream);
+    return;
   }
   if (use_key_split(a, batch, head_dim, causal, policy)) {
     FwdArgs k = a;
@@ -165,8 +162,8 @@ bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int p
 // AUTO takes the 256-row workgroups of 8 waves (one per CU: every K/V tile
 // serves 256 query rows, so each wave issues half the direct loads per step
 // of the 4-wave kernel, which at ~30 cycles of its wave apiece are a tenth or
-// more of a step) for binary16 launches without a
-// mask that neither key split takes and the dynamic schedule would not run:
+// more of a step) for launches without a mask that neither key split takes
+// and the dynamic schedule would not run:
 //  * non-causal launches of at most two 128-row blocks per CU, where the
 //    4-wave kernel leaves some CUs with two workgroups and others with one,
 //    and the 8-wave grid gives each CU at most one (interleaved A/B on
@@ -183,7 +180,7 @@ bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int p
 constexpr int kWideMinRows = 4096;
 
 bool use_wide_workgroups(const FwdArgs& a, int batch, int head_dim, bool causal, int policy) {
-  if (policy != 0 || a.bf16 || has_mask(a)) return false;
+  if (policy != 0 || has_mask(a)) return false;
   if (use_key_split(a, batch, head_dim, causal, policy)) return false;
   FwdArgs planned = a;
   plan_grid(planned, batch, 128);

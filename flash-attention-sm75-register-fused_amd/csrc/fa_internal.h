@@ -115,7 +115,7 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
 // get a CU at once, and for causal head_dim-128 launches whose time is set
 // by their largest query block.
 bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy);
-// Whether AUTO runs a binary16 call without a mask on 256-row workgroups of
+// Whether AUTO runs a call without a mask on 256-row workgroups of
 // 8 waves (non-causal launches of at most two 128-row blocks per CU, and long
 // rows; see fa_fwd.hip).
 bool use_wide_workgroups(const FwdArgs& a, int batch, int head_dim, bool causal, int policy);

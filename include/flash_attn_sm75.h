@@ -213,8 +213,8 @@ int fa_sm75_abi_version(void);
  * query blocks all get a CU at once and for causal head_dim-128 launches
  * small enough that their largest query block sets their time; paired
  * key-split workgroups for causal head_dim-64 launches whose pairs of query
- * blocks all get a CU at once (rows of at least 32 blocks); for binary16
- * calls without a mask, 256-row workgroups of 8 waves for non-causal
+ * blocks all get a CU at once (rows of at least 32 blocks); for calls
+ * without a mask, 256-row workgroups of 8 waves for non-causal
  * launches of at most two 128-row blocks per CU and for rows of at least
  * 4096 queries and keys (causal head_dim 128: 8192) that the dynamic
  * schedule would not run; else 128-row workgroups, with the dynamic

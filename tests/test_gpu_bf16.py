@@ -102,22 +102,25 @@ def test_bf16_peaked_rows(device, B, Hq, Hkv, Nq, Nk, D, causal):
     np.testing.assert_allclose(got, lse_ref, atol=LSE_TOL, rtol=0)
 
 
-def test_bf16_kernels_agree(device):
+@pytest.mark.parametrize("D", [64, 128])
+def test_bf16_kernels_agree(device, D):
     """Every prefill kernel shape and schedule in bfloat16 (forced by the
     policy switch) against the oracle on sampled heads; the static and
-    dynamic schedules bitwise."""
-    B, Hq, Hkv, N, D = 2, 32, 8, 1100, 128
+    dynamic schedules and the 256-row workgroups bitwise against the
+    128-row ones."""
+    B, Hq, Hkv, N = 2, 32, 8, 1100
     q, k, v = seeded((B, Hq, N, D), 4), seeded((B, Hkv, N, D), 5), seeded((B, Hkv, N, D), 6)
     qd, kd, vd = q.to(device), k.to(device), v.to(device)
     outs = {}
     try:
-        for pol in (0, 1, 3, 4, 5):  # auto, 128-row static, dynamic, key split, pairs
+        for pol in (0, 1, 2, 3, 4, 5):  # auto, 128-row, 256-row, dynamic, key split, pairs
             _C.set_kernel_policy(pol)
             outs[pol] = flash_attention_forward_ex(qd, kd, vd, causal=True)
     finally:
         _C.set_kernel_policy(0)
     torch.cuda.synchronize()
     assert torch.equal(outs[1], outs[3])
+    assert torch.equal(outs[1], outs[2])
     group = Hq // Hkv
     for h in (0, 17, 31):
         exp = ref.attention_reference(npf(q[:, h:h + 1]), npf(k[:, h // group:h // group + 1]),

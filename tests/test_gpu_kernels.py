@@ -2,7 +2,8 @@
 
 The prefill kernel comes as 128-row workgroups of 4 waves (two per CU, K/V
 double-buffered; the automatic choice for most launches), 256-row workgroups
-of 8 waves (one per CU, K/V triple-buffered) and 128-row workgroups of 8
+of 8 waves (one per CU, K/V triple-buffered at head_dim 64, double-buffered
+at 128) and 128-row workgroups of 8
 waves whose two groups of 4 split the block's key tiles and merge through LDS
 (one per CU; the automatic choice for launches whose blocks all get a CU at
 once), and the paired form of the latter for causal head_dim-64 launches
