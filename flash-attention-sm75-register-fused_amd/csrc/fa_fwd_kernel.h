@@ -96,6 +96,11 @@ namespace {
 // tail (measured: C3 +3.4%, B=1 Hq=14 Hkv=2 N=4096 +4.8%; launches that keep
 // two waves per SIMD busy throughout lose 1-2%, the extra matrix work costing
 // clock).
+// DYN: the instance carries the dynamic schedule's item loop (4-wave launches
+// that run it).  Static launches take instances without it: the loop's
+// claim, prefetch and hand-off state costs registers all through the steps
+// (the ROWSUM instance: 106 SGPRs spilled to VGPR lanes and 232 VGPRs with
+// it, 15 and 222 without; C3 1.033-1.040x, results bitwise unchanged).
 // LDS through which group 1 of a key split hands its share of a block to
 // group 0: per row wave, MT * 1024 floats of O (four consecutive floats of a
 // lane's accumulator per 16-byte slot), then 64 running maxima and 64 lane
@@ -113,8 +118,9 @@ __device__ __forceinline__ float* pair_exchange() {
 }
 
 template <int D, bool CAUSAL, bool KV_SAME_STRIDE, int WAVES, int MASK_MODE, bool KSPLIT, bool BF16,
-          bool ROWSUM>
+          bool ROWSUM, bool DYN>
 __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) {
+  static_assert(!DYN || (WAVES == 4 && !ROWSUM), "the dynamic schedule runs on 4-wave instances");
   constexpr bool MASK = MASK_MODE != 0;        // an explicit mask: bits or key bytes
   constexpr bool KEY_BYTES = MASK_MODE == 2;   // key-padding bytes (a.mkeys)
   // LDS tile layout: dense (no row padding, 8 direct loads per tile instead
@@ -183,7 +189,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   // and the set of queues it found empty to every wave through LDS: the
   // buffer of V_{STAGES-1}, which no direct load writes between an item's
   // last step and the next item's step 0 (the prologue fills the others).
-  const bool dynamic = WAVES == 4 && a.ctr != nullptr;
+  const bool dynamic = DYN && a.ctr != nullptr;
   const int nq = a.xcds;
   const int per_queue = a.items / nq;
   const int own_q = (int)(__builtin_amdgcn_s_getreg(kHwRegXccId) & 15u) % nq;
@@ -1015,7 +1021,9 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                     ? plan_pairs(args, batch)
                     : plan_grid(args, batch, KSPLIT ? 128 : 32 * WAVES);
   const int64_t slots = resident_fused_workgroups();
-  if (WAVES == 4 && args.ctr != nullptr && use_dynamic_schedule(args, batch, causal, schedule)) {
+  const bool dyn =
+      WAVES == 4 && args.ctr != nullptr && use_dynamic_schedule(args, batch, causal, schedule);
+  if (dyn) {
     launch_clear_tickets(args.ctr, stream);
     wgs = std::min<int64_t>(wgs, slots);
   } else {
@@ -1027,20 +1035,31 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
   }
   const dim3 grid((unsigned)wgs);
   const dim3 block(64 * WAVES);
-#define FA_LAUNCH(C, S, R)                                                                       \
-  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK, KSPLIT, BF16, R>), grid, block, 0, stream, \
-                     args)
-  if (causal) {
-    // Paired single-round launches at head_dim 64 take the ROWSUM instance.
-    if constexpr (D == 64 && WAVES == 4 && !MASK && !KSPLIT) {
-      if (args.pair_half > 0) {
-        if (same) FA_LAUNCH(true, true, true); else FA_LAUNCH(true, false, true);
-        return;
-      }
+#define FA_LAUNCH(C, S, R, Y)                                                                 \
+  hipLaunchKernelGGL((fa_fwd_kernel<D, C, S, WAVES, MASK, KSPLIT, BF16, R, Y>), grid, block, 0,   \
+                     stream, args)
+  // Paired single-round launches at head_dim 64 take the ROWSUM instance
+  // (always static: pair_half is only set without counters).
+  if constexpr (D == 64 && WAVES == 4 && !MASK && !KSPLIT) {
+    if (causal && args.pair_half > 0) {
+      if (same) FA_LAUNCH(true, true, true, false); else FA_LAUNCH(true, false, true, false);
+      return;
     }
-    if (same) FA_LAUNCH(true, true, false); else FA_LAUNCH(true, false, false);
+  }
+  if constexpr (WAVES == 4) {
+    if (dyn) {
+      if (causal) {
+        if (same) FA_LAUNCH(true, true, false, true); else FA_LAUNCH(true, false, false, true);
+      } else {
+        if (same) FA_LAUNCH(false, true, false, true); else FA_LAUNCH(false, false, false, true);
+      }
+      return;
+    }
+  }
+  if (causal) {
+    if (same) FA_LAUNCH(true, true, false, false); else FA_LAUNCH(true, false, false, false);
   } else {
-    if (same) FA_LAUNCH(false, true, false); else FA_LAUNCH(false, false, false);
+    if (same) FA_LAUNCH(false, true, false, false); else FA_LAUNCH(false, false, false, false);
   }
 #undef FA_LAUNCH
 }
