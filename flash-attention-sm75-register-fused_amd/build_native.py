@@ -35,12 +35,14 @@ EXT_NAME = "flash_attn_sm75_cuda"
 # The fused kernel's instances (fa_fwd_d*.hip) are separate translation units
 # so that they compile in parallel.
 HIP_SOURCES = [
-    "fa_fwd_d128.hip", "fa_fwd_d128_mask.hip", "fa_fwd_d128_w8.hip", "fa_fwd_d128_ks.hip",
-    "fa_fwd_d64.hip", "fa_fwd_d64_mask.hip", "fa_fwd_d64_w8.hip", "fa_fwd_d64_ks.hip",
+    "fa_fwd_d128.hip", "fa_fwd_d128_mask.hip", "fa_fwd_d128_w8.hip", "fa_fwd_d128_mask_w8.hip",
+    "fa_fwd_d128_ks.hip",
+    "fa_fwd_d64.hip", "fa_fwd_d64_mask.hip", "fa_fwd_d64_w8.hip", "fa_fwd_d64_mask_w8.hip",
+    "fa_fwd_d64_ks.hip",
     "fa_fwd_d128_bf16.hip", "fa_fwd_d128_mask_bf16.hip", "fa_fwd_d128_w8_bf16.hip",
-    "fa_fwd_d128_ks_bf16.hip",
+    "fa_fwd_d128_mask_w8_bf16.hip", "fa_fwd_d128_ks_bf16.hip",
     "fa_fwd_d64_bf16.hip", "fa_fwd_d64_mask_bf16.hip", "fa_fwd_d64_w8_bf16.hip",
-    "fa_fwd_d64_ks_bf16.hip",
+    "fa_fwd_d64_mask_w8_bf16.hip", "fa_fwd_d64_ks_bf16.hip",
     "fa_fwd_d128_keys.hip", "fa_fwd_d64_keys.hip", "fa_fwd_d128_keys_bf16.hip",
     "fa_fwd_d64_keys_bf16.hip",
     "fa_bwd_d128.hip", "fa_bwd_d64.hip", "fa_bwd_d128_mask.hip", "fa_bwd_d64_mask.hip",

@@ -28,8 +28,8 @@ void launch_shape(const FwdArgs& a, int batch, int head_dim, bool causal, Schedu
 }
 
 // The 8-wave (256-row, one workgroup per CU) kernel runs when asked for
-// (FA_POLICY_WIDE) and where AUTO picks it (use_wide_workgroups); masked calls
-// always take the 4-wave kernel.
+// (FA_POLICY_WIDE) and where AUTO picks it (use_wide_workgroups), also for
+// calls with mask bits; calls with key-padding bytes take the 4-wave kernel.
 template <bool BF16>
 void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int policy,
                   hipStream_t stream) {
@@ -38,11 +38,15 @@ void launch_typed(const FwdArgs& a, int batch, int head_dim, bool causal, int po
     launch_shape<4, 2, false, BF16>(a, batch, head_dim, causal, schedule, stream);
     return;
   }
+  const bool wide = policy == 2 || use_wide_workgroups(a, batch, head_dim, causal, policy);
   if (a.mbits != nullptr) {
-    launch_shape<4, 1, false, BF16>(a, batch, head_dim, causal, schedule, stream);
+    if (wide)
+      launch_shape<8, 1, false, BF16>(a, batch, head_dim, causal, Schedule::kStatic, stream);
+    else
+      launch_shape<4, 1, false, BF16>(a, batch, head_dim, causal, schedule, stream);
     return;
   }
-  if (policy == 2 || use_wide_workgroups(a, batch, head_dim, causal, policy)) {
+  if (wide) {
     launch_shape<8, 0, false, BF16>(a, batch, head_dim, causal, Schedule::kStatic, stream);
     return;
   }
@@ -180,14 +184,17 @@ bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int p
 constexpr int kWideMinRows = 4096;
 
 bool use_wide_workgroups(const FwdArgs& a, int batch, int head_dim, bool causal, int policy) {
-  if (policy != 0 || has_mask(a)) return false;
+  if (policy != 0 || a.mkeys != nullptr) return false;
   if (use_key_split(a, batch, head_dim, causal, policy)) return false;
   FwdArgs planned = a;
   plan_grid(planned, batch, 128);
   if (use_dynamic_schedule(planned, batch, causal, Schedule::kAuto)) return false;
-  if (!causal && planned.items <= 2 * compute_units()) return true;
+  // Mask bits may leave the blocks' work as uneven as a causal launch's (the
+  // causal mask transformers passes as a bool tensor does): the causal rule.
+  const bool uneven = causal || a.mbits != nullptr;
+  if (!uneven && planned.items <= 2 * compute_units()) return true;
   const int rows = std::min(a.n, a.nk);
-  return rows >= kWideMinRows && (head_dim == 64 || !causal || rows >= 2 * kWideMinRows);
+  return rows >= kWideMinRows && (head_dim == 64 || !uneven || rows >= 2 * kWideMinRows);
 }
 
 bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedule schedule) {

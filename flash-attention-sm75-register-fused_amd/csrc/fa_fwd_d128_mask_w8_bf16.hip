@@ -1,0 +1,7 @@
+// Fused forward instances (bfloat16): head_dim 128, 256-row workgroups (8 waves), mask bits.
+#include "fa_fwd_kernel.h"
+
+namespace fa {
+template void launch_fused<128, 8, 1, false, true>(const FwdArgs&, int, bool, Schedule,
+                                                    hipStream_t);
+}  // namespace fa

@@ -336,8 +336,8 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
     // the block sees, [span_lo, span_hi); the tiles outside it hide every
     // key from every row, so skipping them changes no result.  Each lane
     // reads its row's pair (rows past N read row N - 1), the wave and then
-    // the workgroup (through V_1's buffer, which no load writes before step
-    // 0) take the union.
+    // the workgroup (through the buffer of V_{STAGES-1}, which no load writes
+    // before step 0, whose loads follow a barrier) take the union.
     // Dense waves: when every row of the wave sees exactly the interval of
     // its pair (bit 31 of the first entry), the keys [in_lo, in_hi) are
     // visible to all of them, and a tile inside that span needs no mask word
@@ -367,7 +367,7 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
           span_lo = min(span_lo, __shfl_xor(span_lo, d));
           span_hi = max(span_hi, __shfl_xor(span_hi, d));
         }
-        int* const xs = (int*)v_lds1 + 16;
+        int* const xs = (int*)(STAGES == 3 ? v_lds2 : v_lds1) + 16;
         if (lane == 0) {
           xs[2 * wave] = span_lo;
           xs[2 * wave + 1] = span_hi;

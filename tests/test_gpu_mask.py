@@ -456,6 +456,12 @@ RANGE_CASES = [
     (2, 4, 2, 900, 900, 64, False, "window", 0),
     (1, 8, 2, 1100, 1100, 128, False, "holes", 0),
     (2, 4, 4, 700, 700, 128, True, "holes", 3),
+    # 256-row workgroups (policy WIDE), also bitwise against the 128-row kernel
+    (2, 4, 2, 1000, 1000, 128, False, "causal+pad", 2),
+    (3, 8, 2, 700, 700, 64, True, "causal+pad", 2),
+    (2, 4, 2, 513, 513, 128, False, "per-head", 2),
+    (2, 4, 2, 900, 900, 64, False, "window", 2),
+    (1, 8, 2, 1100, 1100, 128, False, "holes", 2),
 ]
 
 
@@ -539,9 +545,14 @@ def test_mask_ranges_skip_tiles(device, B, Hq, Hkv, Nq, Nk, D, bf16, kind, polic
     try:
         o1, l1 = run(True)
         o0, l0 = run(False)
+        if policy == 2:
+            assert lib.fa_sm75_set_kernel_policy(1) == 0
+            on, ln = run(True)
     finally:
         lib.fa_sm75_set_kernel_policy(0)
     assert torch.equal(o1, o0) and torch.equal(l1, l0)
+    if policy == 2:
+        assert torch.equal(o1, on) and torch.equal(l1, ln)
     npf = lambda t: t.float().cpu().numpy()
     mn = np.broadcast_to(m.numpy(), (B, Hq, Nq, Nk))
     if bf16:
