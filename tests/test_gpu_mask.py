@@ -130,6 +130,39 @@ def test_masked_forward_matches_oracle(device, B, Hq, Hkv, Nq, Nk, D, mshape, p,
     np.testing.assert_allclose(got[fin], want[fin], atol=1e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("D,causal,mshape", [
+    (128, True, (2, 1, 700, 700)),
+    (64, "bottom_right", (2, 4, 500, 900)),
+    (64, True, (2, 1, 700, 700)),
+    (128, False, (700, 700)),
+])
+def test_masked_wide_matches_narrow(device, D, causal, mshape):
+    """Mask bits (packed with ranges by the binding) with and without the
+    causal flag on 256-row workgroups (policy WIDE): bitwise equal to the
+    128-row kernel (policy NARROW) and within the oracle's bar."""
+    import flash_attn_sm75_cuda as _C
+    B, Hq, Hkv = 2, 4, 2
+    Nq, Nk = mshape[-2], mshape[-1]
+    print(f"[wide mask] D={D} causal={causal} mask={mshape}", flush=True)
+    q, k, v = seeded((B, Hq, Nq, D), 21), seeded((B, Hkv, Nk, D), 22), seeded((B, Hkv, Nk, D), 23)
+    m = rand_mask(mshape, 0.8, 24)
+    outs = {}
+    try:
+        for pol in (2, 1):
+            _C.set_kernel_policy(pol)
+            outs[pol] = flash_attention_forward_ex(q.to(device), k.to(device), v.to(device),
+                                                   causal=causal, return_lse=True,
+                                                   attn_mask=m.to(device))
+    finally:
+        _C.set_kernel_policy(0)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[2][0], outs[1][0]) and torch.equal(outs[2][1], outs[1][1])
+    code = {False: 0, True: 1, "bottom_right": 2}[causal]
+    expect = ref.attention_reference_chunked(q.numpy(), k.numpy(), v.numpy(), causal=code,
+                                             attn_mask=m.numpy(), return_f32=True)
+    assert_parity(outs[2][0], expect, "wide masked")
+
+
 def test_all_true_mask_equals_no_mask(device):
     q, k, v = (seeded((2, 8, 333, 128), s).to(device) for s in (6, 7, 8))
     ones = torch.ones(333, 333, dtype=torch.bool, device=device)
