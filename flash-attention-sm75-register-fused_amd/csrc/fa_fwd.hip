@@ -112,12 +112,19 @@ int64_t tile_steps_per_head(const FwdArgs& a, bool causal) {
 constexpr int64_t kDynamicMinSteps = 1024;
 
 // AUTO takes key-split workgroups (8 waves on one 128-row block, one per CU)
-//  * for every launch whose blocks all get a CU at once: there a 4-wave
-//    workgroup would run alone on its CU, one wave per SIMD, where its
-//    steps are bound by latency; two waves per SIMD on half the key tiles
-//    each finish the block sooner.  Measured on MI355X (interleaved A/B
-//    against AUTO's 4-wave kernel, head_dim 64 and 128, full and causal,
-//    B=1 H=8 N=2048/4096 and B=1 H=32 N=512/1024): 1.02-1.22x;
+//  * for launches whose blocks all get a CU at once and whose rows are long
+//    enough (split_pays): there a 4-wave workgroup runs alone on its CU, one
+//    wave per SIMD, where its steps are bound by latency; two waves per SIMD
+//    on half the key tiles each finish the block sooner, unless the rows
+//    are short next to the merge through LDS.  Measured on MI355X
+//    (interleaved A/B against the 4-wave kernel's static instance, 21
+//    shapes): non-causal head_dim 64 from 16 key tiles 1.053-1.149x (8
+//    tiles 0.972x); non-causal head_dim 128 from 24 tiles 1.051-1.078x, or
+//    with at most a quarter of the CUs busy 1.099x (16 tiles on 128 or 256
+//    blocks 1.003x / 0.968x, 8 tiles 0.920x); causal head_dim 128
+//    1.011-1.242x; causal head_dim 64 with rows of 64 tiles 1.017x (16-32
+//    tiles 0.934-0.990x).  Declined launches take the 4-wave kernel (the
+//    256-row one runs them at 0.66-0.69x);
 //  * at head_dim 128 for causal launches of at most this many 128-row
 //    blocks per resident 128-row workgroup, each block row at least
 //    kSplitMinBlocks long: the largest block's chain of key tiles sets the
@@ -157,7 +164,14 @@ bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int p
   if (policy != 0) return false;
   FwdArgs planned = a;
   plan_grid(planned, batch, 128);
-  if (planned.items <= compute_units()) return true;
+  if (planned.items <= compute_units()) {
+    const int tiles = (a.nk + 63) / 64;  // key tiles of the longest block row
+    const bool split_pays =
+        causal ? head_dim == 128 || tiles >= 64
+               : head_dim == 64 ? tiles >= 16
+                                : tiles >= 24 || planned.items <= compute_units() / 4;
+    return split_pays;
+  }
   if (use_pair_split(a, batch, head_dim, causal, policy)) return true;
   return causal && head_dim == 128 && planned.num_qblocks >= kSplitMinBlocks &&
          planned.items <= kSplitMaxItems * resident_fused_workgroups();
@@ -166,17 +180,23 @@ bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int p
 // AUTO takes the 256-row workgroups of 8 waves (one per CU: every K/V tile
 // serves 256 query rows, so each wave issues half the direct loads per step
 // of the 4-wave kernel, which at ~30 cycles of its wave apiece are a tenth or
-// more of a step) for launches without a mask that neither key split takes
-// and the dynamic schedule would not run:
-//  * non-causal launches of at most two 128-row blocks per CU, where the
-//    4-wave kernel leaves some CUs with two workgroups and others with one,
-//    and the 8-wave grid gives each CU at most one (interleaved A/B on
-//    MI355X: C2 1.084x, B=3 H=16 N=1024 1.087x at head_dim 64 and 1.060x at
-//    128, B=2 H=24 N=1024 1.104x; B=4 H=12 N=1536, past two, 0.836x);
-//  * rows of at least kWideMinRows queries and keys, non-causal or at
-//    head_dim 64 (1.01-1.07x over 13 shapes, the worst 0.989x, B=2 Hq=32
-//    Hkv=8 N=4096 d64 causal), or causal head_dim 128 from twice that (C4
-//    1.010x, B=2 Hq=32 Hkv=8 N=8192 1.000x; at N=4096 0.971-1.004x).
+// more of a step) for launches without key-padding bytes that neither key
+// split takes and the dynamic schedule would not run (interleaved A/B on
+// MI355X against the 4-wave kernel's static instances):
+//  * non-causal launches of more than one and at most two 128-row blocks
+//    per CU, where the 4-wave kernel leaves some CUs with two workgroups and
+//    others with one, and the 8-wave grid gives each CU at most one (with
+//    at most one block per CU, 0.66-0.69x; C2 1.044x, B=3 H=16
+//    N=1024 1.038x at head_dim 64 and 1.041x at 128, B=2 H=24 N=1024 d128
+//    1.040x; B=4 H=12 N=1536, past two, 0.836x);
+//  * rows of at least kWideMinRows queries and keys: causal (or with mask
+//    bits, which may leave the blocks' work as uneven as the causal flag,
+//    as transformers' causal bool mask does) at head_dim 64 (1.019-1.037x
+//    over three shapes), non-causal at head_dim 128 (1.018-1.035x), and
+//    causal head_dim 128 from twice that (C4 1.021x, B=2 Hq=32 Hkv=8
+//    N=8192 1.003x).  Non-causal head_dim-64 rows stay on the 4-wave
+//    kernel, whose static instance holds 168 VGPRs (0.914-1.003x over eight
+//    shapes on 256-row workgroups).
 // Shorter rows stay on the 4-wave kernel: its causal large/small pairing
 // evens single-round launches out (C3 0.825x on 256-row workgroups), and the
 // 256-row blocks' diagonal costs more of a short row (B=4 Hq=32 Hkv=8 N=2048
@@ -189,12 +209,12 @@ bool use_wide_workgroups(const FwdArgs& a, int batch, int head_dim, bool causal,
   FwdArgs planned = a;
   plan_grid(planned, batch, 128);
   if (use_dynamic_schedule(planned, batch, causal, Schedule::kAuto)) return false;
-  // Mask bits may leave the blocks' work as uneven as a causal launch's (the
-  // causal mask transformers passes as a bool tensor does): the causal rule.
   const bool uneven = causal || a.mbits != nullptr;
-  if (!uneven && planned.items <= 2 * compute_units()) return true;
+  if (!uneven && planned.items > compute_units() && planned.items <= 2 * compute_units())
+    return true;
   const int rows = std::min(a.n, a.nk);
-  return rows >= kWideMinRows && (head_dim == 64 || !uneven || rows >= 2 * kWideMinRows);
+  if (rows < kWideMinRows) return false;
+  return head_dim == 64 ? uneven : !uneven || rows >= 2 * kWideMinRows;
 }
 
 bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedule schedule) {

@@ -216,8 +216,9 @@ int fa_sm75_abi_version(void);
  * blocks all get a CU at once (rows of at least 32 blocks); for calls
  * without key-padding bytes, 256-row workgroups of 8 waves for non-causal
  * launches of at most two 128-row blocks per CU and for rows of at least
- * 4096 queries and keys (causal head_dim 128: 8192; calls with mask bits
- * take the causal rule) that the dynamic schedule would not run; else 128-row workgroups, with the dynamic
+ * 4096 queries and keys (causal or with mask bits at head_dim 64;
+ * non-causal at 128, causal from 8192) that the dynamic schedule would not
+ * run; else 128-row workgroups, with the dynamic
  * XCD-balanced schedule for long launches when p->workspace holds its
  * counters.  NARROW forces 128-row workgroups of 4 waves (two per CU) on
  * the static schedule (one workgroup per query block); WIDE forces 256-row
