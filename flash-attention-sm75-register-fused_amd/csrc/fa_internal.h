@@ -97,7 +97,8 @@ inline int64_t plan_pairs(FwdArgs& a, int batch) {
   return a.items;
 }
 // Whether the 4-wave kernel runs the dynamic schedule for a planned call
-// (plan_grid done, 128-row blocks), given counters to run it with.
+// (plan_grid done, 128-row blocks), given counters to run it with (on its
+// instances that carry the item loop, DYN).
 bool use_dynamic_schedule(const FwdArgs& planned, int batch, bool causal, Schedule schedule);
 // Workspace bytes the fused path uses for a call (the dynamic schedule's
 // counters, or 0), under a kernel policy.
@@ -112,12 +113,13 @@ void launch_fused(const FwdArgs& a, int batch, bool causal, Schedule schedule,
                   hipStream_t stream);
 // Whether a call runs on key-split workgroups: policy 4 or 5, or AUTO for
 // launches whose blocks (or, causal at head_dim 64, pairs of blocks) all
-// get a CU at once, and for causal head_dim-128 launches whose time is set
-// by their largest query block.
+// get a CU at once and whose rows are long enough to pay for the merge, and
+// for causal head_dim-128 launches whose time is set by their largest query
+// block.
 bool use_key_split(const FwdArgs& a, int batch, int head_dim, bool causal, int policy);
-// Whether AUTO runs a call without a mask on 256-row workgroups of
-// 8 waves (non-causal launches of at most two 128-row blocks per CU, and long
-// rows; see fa_fwd.hip).
+// Whether AUTO runs a call without key-padding bytes on 256-row workgroups
+// of 8 waves (non-causal launches of more than one and at most two 128-row
+// blocks per CU, and long rows; see fa_fwd.hip).
 bool use_wide_workgroups(const FwdArgs& a, int batch, int head_dim, bool causal, int policy);
 // Whether key-split workgroups take pairs of query blocks (causal head_dim
 // 64: policy 5, or AUTO when the blocks outnumber the CUs but the pairs do

@@ -210,12 +210,15 @@ int fa_sm75_abi_version(void);
 /* Fused-kernel selection, process-wide (no reference counterpart: a tuning
  * and testing control).  AUTO picks by problem size: the split-K path for
  * few query rows per K/V head; key-split workgroups for launches whose
- * query blocks all get a CU at once and for causal head_dim-128 launches
- * small enough that their largest query block sets their time; paired
+ * query blocks all get a CU at once (where the rows are long enough:
+ * non-causal from 16 key tiles at head_dim 64 and 24 at 128 or with at most
+ * a quarter of the CUs busy, causal at head_dim 128, causal head_dim 64 from
+ * 64) and for causal head_dim-128 launches small enough that their largest query block sets their time; paired
  * key-split workgroups for causal head_dim-64 launches whose pairs of query
  * blocks all get a CU at once (rows of at least 32 blocks); for calls
  * without key-padding bytes, 256-row workgroups of 8 waves for non-causal
- * launches of at most two 128-row blocks per CU and for rows of at least
+ * launches of more than one and at most two 128-row blocks per CU and for
+ * rows of at least
  * 4096 queries and keys (causal or with mask bits at head_dim 64;
  * non-causal at 128, causal from 8192) that the dynamic schedule would not
  * run; else 128-row workgroups, with the dynamic
