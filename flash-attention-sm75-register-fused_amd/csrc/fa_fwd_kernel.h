@@ -172,8 +172,8 @@ __global__ void __launch_bounds__(64 * WAVES, 2) fa_fwd_kernel(const FwdArgs a) 
   const int gofs = kgrp * L::Tile;             // its LDS tiles' offset
 
   // Work items.  Static schedule (a.ctr == nullptr): workgroup wg does item
-  // wg.  Dynamic schedule (4-wave kernel, a.ctr set, grid = resident
-  // workgroups): the items form a.xcds queues, queue x holding the items the
+  // wg.  Dynamic schedule (the 4-wave kernel's DYN instances, a.ctr set,
+  // grid = resident workgroups): the items form a.xcds queues, queue x holding the items the
   // static schedule gives XCD x, one (batch, KV head) unit after the other
   // and largest first within each (block_work's unit_major order).  A
   // workgroup takes items from the head of its own XCD's queue; once that is
