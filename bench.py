@@ -611,6 +611,61 @@ def time_hf(prompt_len=4096, decode_steps=32):
     return res
 
 
+def ab_policies(policies, shapes, rounds=4, steps=30, warm_ms=40.0, dtype="fp16"):
+    """Kernel policies timed interleaved in one process on each shape (the
+    comparison behind AUTO's selection rules): per round and policy, launches
+    for warm_ms, then `steps` launches back to back between one HIP event
+    pair; the best round per policy is reported, with the output's largest
+    difference from the first policy's (0: bitwise equal).  Shapes are
+    B,Hq,Hkv,N,D,causal[,Nk] (causal 2: bottom-right); N(0,1) data."""
+    import torch
+
+    import flash_attn_sm75_cuda as _C
+    from flash_attention_sm75 import flash_attention_forward_ex
+
+    dev = torch.device("cuda", 0)
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    stream = torch.cuda.current_stream()
+    causal_of = {0: False, 1: True, 2: "bottom_right"}
+    try:
+        for shape in shapes:
+            vals = [int(x) for x in shape.split(",")]
+            B, Hq, Hkv, N, D, c = vals[:6]
+            NK = vals[6] if len(vals) > 6 else N
+            g = torch.Generator("cpu").manual_seed(11)
+            q = torch.randn(B, Hq, N, D, generator=g).to(dt).to(dev)
+            k = torch.randn(B, Hkv, NK, D, generator=g).to(dt).to(dev)
+            v = torch.randn(B, Hkv, NK, D, generator=g).to(dt).to(dev)
+            causal = causal_of[c]
+            best = {p_: float("inf") for p_ in policies}
+            outs = {}
+            for _ in range(rounds):
+                for p_ in policies:
+                    _C.set_kernel_policy(p_)
+                    t0 = time.perf_counter()
+                    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+                        for _ in range(10):
+                            outs[p_] = flash_attention_forward_ex(q, k, v, causal=causal)
+                        torch.cuda.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    for _ in range(steps):
+                        flash_attention_forward_ex(q, k, v, causal=causal)
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                    best[p_] = min(best[p_], e0.elapsed_time(e1) / steps * 1e3)
+            F = flops(B, Hq, N, D, bool(c)) * NK / N
+            ref_o = outs[policies[0]].float()
+            cols = " | ".join(
+                f"policy {p_} {best[p_]:8.2f} us {F / best[p_] / 1e6:7.1f} TFLOPS "
+                f"diff {(outs[p_].float() - ref_o).abs().max().item():.1e}" for p_ in policies)
+            print(f"{shape:>24s} {dtype}: {cols} | ratio first/last "
+                  f"{best[policies[0]] / best[policies[-1]]:.3f}", flush=True)
+            del q, k, v, outs
+    finally:
+        _C.set_kernel_policy(0)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -649,6 +704,14 @@ def main():
                     help="skip the reference's head_dim sweep (d64/d128 x N x full/causal)")
     ap.add_argument("--no-widened", action="store_true",
                     help="skip timing the widened calls (bf16, boolean mask, chunked prefill)")
+    ap.add_argument("--ab-policies", default=None,
+                    help="diagnostic: time these kernel policies interleaved (e.g. 1,2,0) on "
+                         "--ab-shapes and exit (no JSON line); the comparisons behind AUTO's "
+                         "selection rules")
+    ap.add_argument("--ab-shapes", default="1,32,8,8192,128,1",
+                    help="';'-separated B,Hq,Hkv,N,D,causal[,Nk] (causal 2: bottom-right)")
+    ap.add_argument("--ab-rounds", type=int, default=4)
+    ap.add_argument("--ab-dtype", default="fp16", choices=("fp16", "bf16"))
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise copy of 256 MiB (known HBM bytes) "
                          "to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
@@ -660,6 +723,11 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.ab_policies:
+        ab_policies([int(x) for x in args.ab_policies.split(",")], args.ab_shapes.split(";"),
+                    rounds=args.ab_rounds, dtype=args.ab_dtype)
+        return
 
     cfg = args.config
     if args.shape:
