@@ -198,13 +198,20 @@ __device__ __forceinline__ void fence_schedule() { __builtin_amdgcn_sched_barrie
 
 // Workgroup barrier after which all but this wave's last N direct-to-LDS
 // loads have landed (vmcnt counts them, and they complete in order), so the
-// tiles they wrote are visible to every wave.  The compiler does not wait
-// for direct loads before s_barrier on its own.
+// tiles they wrote are visible to every wave, and every wave's LDS reads and
+// writes before it are done (lgkmcnt 0).  The compiler does not wait for
+// direct loads before s_barrier on its own.  __syncthreads() is not used: its
+// workgroup fence counts direct loads as LDS writes and so adds a full
+// vmcnt(0), which would drain the loads a multi-stage pipeline keeps in
+// flight.  The empty asm statements with a memory clobber keep the compiler
+// from moving memory accesses across the barrier, which the fence did.
 template <int N>
 __device__ __forceinline__ void barrier_after_loads() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 template <bool B>
